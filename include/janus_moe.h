@@ -1,0 +1,133 @@
+/*
+ * janus_moe.h - C ABI of the MI355X (gfx950) W4A16 mixture-of-experts layer.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t, launches its kernels on that stream
+ * and returns at once: no allocation, no host synchronisation, no device-to-host read. Scratch memory comes from
+ * the caller through `ws` / `ws_bytes` (ask the matching *_workspace_bytes function for the size). The calls are
+ * re-entrant; the only process state is a thread-local error string. Return value 0 is success; any other value
+ * is an error code below, with a message in janus_moe_last_error().
+ *
+ * Tensor conventions (row-major, innermost dimension last, no padding):
+ *   bf16 values travel as uint16_t bit patterns.
+ *   int4 weights: int32 words [rows, K/8]; element k = 8*j + i of a row lives in bits 4i..4i+3 of word j, two's
+ *   complement in [-8, 7]. Scales: bf16 [rows, K/128], one per 128 consecutive k. The weight value is
+ *   bf16(float(q) * float(scale)), rounded to nearest even once.
+ *   Expert stacks: gate_up words [E, 2I, H/8] (rows 0..I-1 gate, I..2I-1 up), scales [E, 2I, H/128];
+ *   down words [E, H, I/8], scales [E, H, I/128].
+ */
+#ifndef JANUS_MOE_H
+#define JANUS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define JANUS_MOE_API __attribute__((visibility("default")))
+#else
+#define JANUS_MOE_API
+#endif
+
+typedef struct ihipStream_t* janus_stream_t; /* the same handle type as hipStream_t */
+
+enum {
+  JANUS_MOE_OK = 0,
+  JANUS_MOE_EINVAL = 1,     /* a size, shape or pointer argument is not supported */
+  JANUS_MOE_EWORKSPACE = 2, /* ws_bytes is smaller than the matching *_workspace_bytes() */
+  JANUS_MOE_ELAUNCH = 3     /* the HIP runtime refused a launch */
+};
+
+/* Message of the last failing call on this thread ("" when none). */
+JANUS_MOE_API const char* janus_moe_last_error(void);
+/* Bumped whenever a signature below changes. */
+JANUS_MOE_API int janus_moe_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Router.
+ * janus_moe_router_prepare has no counterpart in the reference: it splits the fp32 router weight [E, H] once
+ * into two bf16 planes plus the norms the selection uses (a layout transform of a fixed weight, done at load
+ * time). `prep` is device memory of janus_moe_router_prep_bytes(E, H) bytes.
+ */
+JANUS_MOE_API size_t janus_moe_router_prep_bytes(int E, int H);
+JANUS_MOE_API int janus_moe_router_prepare(const float* w_router, int E, int H, void* prep, size_t prep_bytes,
+                             janus_stream_t stream);
+
+/* Replaces Qwen3_5MoeTopKRouter.forward (transformers models/qwen3_5_moe/modeling_qwen3_5_moe.py:768-776)
+ * plus the shared-expert gate sigmoid (same file :794).
+ *   x [T, H] bf16, w_router [E, H] fp32, prep from janus_moe_router_prepare, bias [E] fp32 or NULL (added to
+ *   the logits), w_shared_gate [H] bf16 or NULL.
+ *   Outputs: topk_idx [T, top_k] int32 (slot order: logit descending, ties to the lower expert id),
+ *   topk_w [T, top_k] fp32 (softmax over the logits renormalised over the top_k), gamma [T] fp32 =
+ *   sigmoid(x . w_shared_gate) (ignored when w_shared_gate is NULL).
+ *   Logit of (t, e): the fp32 rounding (nearest even) of the exact dot product x[t] . w_router[e], plus bias[e]
+ *   in fp32. Selection and slot order are bit-exact under that rule. */
+JANUS_MOE_API size_t janus_moe_route_workspace_bytes(int T, int H, int E);
+JANUS_MOE_API int janus_moe_route(const uint16_t* x, const float* w_router, const void* prep, const float* bias,
+                    const uint16_t* w_shared_gate, int T, int H, int E, int top_k, int32_t* topk_idx,
+                    float* topk_w, float* gamma, void* ws, size_t ws_bytes, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces align(top_k_index, num_experts, block) (janus/moe_w4a16.py:89-106), bit-exact:
+ *   top_k_index [S, top_k] int64 with values in [0, E);
+ *   sorted_ids [tiles * block] int64, expert_ids [tiles] int64, total [1] int64, where
+ *   tiles = (S*top_k + E*(block-1) + block - 1) / block. Assignment ids sorted stably by expert, each expert
+ *   padded to a multiple of `block` with the sentinel S*top_k; expert_ids[i] = the expert owning rows
+ *   [i*block, (i+1)*block), E or more past `total`; total = the padded row count. */
+JANUS_MOE_API size_t janus_moe_align_workspace_bytes(int S, int top_k, int E);
+JANUS_MOE_API int janus_moe_align(const int64_t* top_k_index, int S, int top_k, int E, int block, int64_t* sorted_ids,
+                    int64_t* expert_ids, int64_t* total, void* ws, size_t ws_bytes, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces fused_moe(x, top_k_index, top_k_weights, gate_up, ..., down, ...) (janus/moe_w4a16.py:122-140) and
+ * NVFP4Experts.forward (janus/hybrid.py:551-572) for the int4 group-128 codec:
+ *   out[s] = bf16( sum_j top_k_weights[s, j] * down_e( bf16(silu(gate_e(x[s])) * up_e(x[s])) ) ), e =
+ *   top_k_index[s, j]; every dot product accumulates in fp32, the weighted sum over j is fp32 and rounded once.
+ *   x [S, H] bf16, top_k_index [S, top_k] int64, top_k_weights [S, top_k] fp32, out [S, H] bf16.
+ *   Requires H % 128 == 0 and I % 128 == 0. */
+JANUS_MOE_API size_t janus_moe_experts_workspace_bytes(int S, int top_k, int E, int H, int I);
+JANUS_MOE_API int janus_moe_experts(const uint16_t* x, const int64_t* top_k_index, const float* top_k_weights,
+                      const int32_t* gate_up_q, const uint16_t* gate_up_s, const int32_t* down_q,
+                      const uint16_t* down_s, int S, int H, int I, int E, int top_k, uint16_t* out, void* ws,
+                      size_t ws_bytes, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces the dequantising properties NVFP4Experts.gate_up_proj / down_proj and NVFP4Linear.weight
+ * (janus/hybrid.py:539-545, 502-504) for the int4 codec: out [rows, K] bf16 = bf16(q * s), computed by the same
+ * device decode the GEMMs use. q [rows, K/8] int32, s [rows, K/128] bf16; K % 128 == 0. Stacks [E, N, K] are
+ * rows = E * N. */
+JANUS_MOE_API int janus_moe_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out,
+                                    janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces Qwen3_5MoeSparseMoeBlock.forward (transformers models/qwen3_5_moe/modeling_qwen3_5_moe.py:787-798)
+ * with int4 expert and shared-expert weights: router, routed experts, shared expert scaled by
+ * sigmoid(x . shared_gate), all summed in fp32 and rounded to bf16 once. */
+typedef struct janus_moe_block_weights {
+  int H, I, E, top_k;             /* hidden, routed intermediate, experts, experts per token */
+  int I_s;                        /* shared-expert intermediate; 0 = no shared expert */
+  const float* router_w;          /* [E, H] fp32 */
+  const void* router_prep;        /* janus_moe_router_prepare(router_w) */
+  const float* router_bias;       /* [E] fp32 or NULL */
+  const int32_t* gate_up_q;       /* [E, 2I, H/8] */
+  const uint16_t* gate_up_s;      /* [E, 2I, H/128] */
+  const int32_t* down_q;          /* [E, H, I/8] */
+  const uint16_t* down_s;         /* [E, H, I/128] */
+  const int32_t* sh_gate_up_q;    /* [2 I_s, H/8] */
+  const uint16_t* sh_gate_up_s;   /* [2 I_s, H/128] */
+  const int32_t* sh_down_q;       /* [H, I_s/8] */
+  const uint16_t* sh_down_s;      /* [H, I_s/128] */
+  const uint16_t* sh_gate_w;      /* [H] bf16 (shared_expert_gate.weight) */
+} janus_moe_block_weights;
+
+/* topk_idx / topk_w: optional [T, top_k] copies of the routing (NULL to skip). */
+JANUS_MOE_API size_t janus_moe_block_workspace_bytes(int T, int H, int I, int E, int top_k, int I_s);
+JANUS_MOE_API int janus_moe_block_forward(const janus_moe_block_weights* w, const uint16_t* x, int T, uint16_t* out,
+                            int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JANUS_MOE_H */

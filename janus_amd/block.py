@@ -1,0 +1,122 @@
+"""Qwen3_5MoeSparseMoeBlock counterpart (transformers models/qwen3_5_moe/modeling_qwen3_5_moe.py:704-798) with int4
+experts and shared expert: `gate` (router), `experts` (W4A16Experts), `shared_expert` (gate_proj / up_proj /
+down_proj) and `shared_expert_gate`, so callers that test `hasattr(layer.mlp, "experts")` (janus/hybrid.py:1028,
+1100, 1714) keep working.
+
+Under inference on a GPU (JANUS_MOE_KERNEL unset or `fused`) forward is one `janus_moe::block_forward` call: router,
+routed experts and the gated shared expert summed in fp32 and rounded to the output dtype once. Otherwise it composes
+the submodules exactly as the HF block does (each part rounding to the activation dtype, a bf16 final add).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+from .hybrid import W4A16Experts, W4A16Linear, moe_kernel
+
+
+class W4A16TopKRouter(nn.Module):
+    """Qwen3_5MoeTopKRouter: weight [E, H] fp32, forward(h) -> (router_logits [T, E] fp32, scores [T, k], indices
+    [T, k] int64). On the GPU the selection is the exact rule of the route op: the k largest correctly rounded fp32
+    logits, ties to the lower expert id, slots in descending order; scores are the softmax renormalised over the top-k.
+    `bias` (optional [E] fp32) is added to the logits before selection."""
+
+    def __init__(self, weight: torch.Tensor, top_k: int, bias: torch.Tensor | None = None):
+        super().__init__()
+        self.weight = nn.Parameter(weight.float(), requires_grad=False)
+        self.register_buffer("bias", None if bias is None else bias.float(), persistent=False)
+        self.top_k, self.num_experts, self.hidden_dim = top_k, weight.shape[0], weight.shape[1]
+        self._prep, self._prep_key = None, None
+
+    def prep(self) -> torch.Tensor:
+        """The route op's split of the weight, rebuilt when the weight changes."""
+        w = self.weight
+        key = (w.data_ptr(), w._version, w.device)
+        if self._prep_key != key:
+            self._prep, self._prep_key = ops.router_prepare(w.detach().contiguous()), key
+        return self._prep
+
+    def forward(self, hidden_states):
+        x = hidden_states.reshape(-1, self.hidden_dim)
+        logits = F.linear(x.float(), self.weight)
+        if self.bias is not None:
+            logits = logits + self.bias
+        if x.is_cuda and not torch.is_grad_enabled():
+            idx, w, _ = ops.route(x.to(torch.bfloat16).contiguous(), self.weight, self.prep(), self.bias, None,
+                                  self.top_k)
+            return logits, w, idx.long()
+        probs = torch.softmax(logits, dim=-1, dtype=torch.float)
+        top, idx = torch.topk(probs, self.top_k, dim=-1)
+        top = top / top.sum(dim=-1, keepdim=True)
+        return logits, top, idx
+
+
+class W4A16MLP(nn.Module):
+    """Qwen3_5MoeMLP with packed weights: gate_up words [2 I_s, H/8] and scales (gate rows first), down [H, I_s/8];
+    gate_proj / up_proj / down_proj are W4A16Linear views of them."""
+
+    def __init__(self, gate_up, gate_up_scale, down, down_scale, act_fn=F.silu):
+        super().__init__()
+        self.register_buffer("gate_up", gate_up, persistent=False)
+        self.register_buffer("gate_up_scale", gate_up_scale, persistent=False)
+        self.register_buffer("down", down, persistent=False)
+        self.register_buffer("down_scale", down_scale, persistent=False)
+        I_s = gate_up.shape[0] // 2
+        self.intermediate_size, self.hidden_size = I_s, gate_up.shape[1] * 8
+        self.gate_proj = W4A16Linear(gate_up[:I_s], gate_up_scale[:I_s])
+        self.up_proj = W4A16Linear(gate_up[I_s:], gate_up_scale[I_s:])
+        self.down_proj = W4A16Linear(down, down_scale)
+        self.act_fn = act_fn
+
+    def forward(self, x):
+        return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+
+
+class W4A16SparseMoeBlock(nn.Module):
+    """forward(hidden_states [B, L, H]) -> [B, L, H] (or [T, H] -> [T, H])."""
+
+    def __init__(self, gate: W4A16TopKRouter, experts: W4A16Experts, shared_expert: W4A16MLP | None,
+                 shared_expert_gate: nn.Linear | None):
+        super().__init__()
+        self.gate, self.experts = gate, experts
+        self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
+
+    @classmethod
+    def from_tensors(cls, w: dict, top_k: int, dtype=torch.bfloat16) -> "W4A16SparseMoeBlock":
+        """Builds the block from a `janus_amd.synth.layer` dict (same layouts)."""
+        router = W4A16TopKRouter(w["router_w"], top_k, w.get("router_bias"))
+        experts = W4A16Experts(w["gate_up_q"], w["gate_up_s"], None, w["down_q"], w["down_s"], None)
+        shared, shared_gate = None, None
+        if w.get("sh_gate_up_q") is not None:
+            shared = W4A16MLP(w["sh_gate_up_q"], w["sh_gate_up_s"], w["sh_down_q"], w["sh_down_s"])
+            H = w["router_w"].shape[1]
+            shared_gate = nn.Linear(H, 1, bias=False, dtype=dtype)
+            with torch.no_grad():
+                shared_gate.weight.copy_(w["sh_gate_w"].reshape(1, H).to(dtype))
+            shared_gate.weight.requires_grad_(False)
+        return cls(router, experts, shared, shared_gate)
+
+    def forward(self, hidden_states):
+        shape = hidden_states.shape
+        x = hidden_states.reshape(-1, shape[-1])
+        if x.is_cuda and not torch.is_grad_enabled() and moe_kernel(x.device) == "fused":
+            sh = self.shared_expert
+            out, _, _ = ops.block_forward(
+                x.to(torch.bfloat16).contiguous(), self.gate.weight, self.gate.prep(), self.gate.bias,
+                self.experts.gate_up, self.experts.gate_up_scale, self.experts.down, self.experts.down_scale,
+                None if sh is None else sh.gate_up, None if sh is None else sh.gate_up_scale,
+                None if sh is None else sh.down, None if sh is None else sh.down_scale,
+                None if self.shared_expert_gate is None else
+                self.shared_expert_gate.weight.reshape(-1).to(torch.bfloat16).contiguous(),
+                self.gate.top_k)
+            return out.to(hidden_states.dtype).reshape(shape)
+        _, weights, idx = self.gate(x)
+        out = self.experts(x, idx, weights.to(x.dtype))
+        if self.shared_expert is not None:
+            shared = self.shared_expert(x)
+            if self.shared_expert_gate is not None:
+                shared = torch.sigmoid(self.shared_expert_gate(x)) * shared
+            out = out + shared
+        return out.reshape(shape)

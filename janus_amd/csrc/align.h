@@ -1,0 +1,28 @@
+// Internal interface of the align kernels (align.hip), shared with the pipelines that build a GEMM chunk list.
+#pragma once
+
+#include "common.h"
+
+namespace janus {
+
+constexpr int kMaxExperts = 1024;  // one scan thread per expert
+constexpr int kAlignChunk = 1024;  // assignments per rank/scatter block
+
+struct AlignWorkspace {
+  int* hist;        // [nb][E] per-block counts, then per-block offsets
+  int* local_rank;  // [A]
+  int* counts;      // [E]
+  int* start;       // [E] padded start of each expert's rows
+};
+
+AlignWorkspace carve_align(Carver& c, int A, int E);
+
+// sorted_ids [sorted_len] is filled with the sentinel A, then the permutation. Either expert_ids/total (reference tile
+// plan, `tiles` entries) or chunks/num_chunks (runs of at most chunk_rows rows of one expert) may be null. zero_buf, if
+// given, is cleared (zero_len floats, a multiple of 4) by the first launch.
+template <typename IdxT, typename OutT>
+int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
+                 OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
+                 float* zero_buf, long zero_len, hipStream_t stream);
+
+}  // namespace janus

@@ -1,0 +1,215 @@
+// Pipelines behind the experts and block entry points, workspace layouts, and the error channel.
+//
+// experts (fused_moe, janus/moe_w4a16.py:122-140):   align -> gate_up -> down (+ combine) -> finalize
+// block   (Qwen3_5MoeSparseMoeBlock.forward):        route -> align -> gate_up (+ shared) -> down (+ shared, combine)
+//                                                     -> finalize
+// Every launch goes on the caller's stream; counts stay on the device (grids are sized for the worst case and idle
+// workgroups exit), so a caller can capture the whole sequence in a HIP graph.
+#include <stdarg.h>
+
+#include "align.h"
+#include "gemm.h"
+#include "router.h"
+
+namespace janus {
+
+namespace {
+thread_local char g_error[512] = "";
+}
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+namespace {
+
+struct ExpertsWorkspace {
+  AlignWorkspace align;
+  int* sorted_ids;  // [P] permuted assignment ids, sentinel A
+  int4* chunks;     // [C]
+  int* num_chunks;  // [1]
+  uint16_t* h;      // [P, I]
+  uint16_t* h_sh;   // [T, I_s]
+  float* acc;       // [T, H]
+  int P, C;
+};
+
+ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I, int I_s) {
+  ExpertsWorkspace w;
+  const int A = T * top_k;
+  w.P = A + E * (kRowPad - 1);
+  w.C = ceil_div(A, kChunkRows) + E;
+  w.align = carve_align(c, A, E);
+  w.sorted_ids = c.take<int>(w.P);
+  w.chunks = c.take<int4>(w.C);
+  w.num_chunks = c.take<int>(1);
+  w.h = c.take<uint16_t>((size_t)w.P * I);
+  w.h_sh = c.take<uint16_t>((size_t)T * I_s);
+  w.acc = c.take<float>((size_t)T * H);
+  return w;
+}
+
+int check_expert_sizes(const char* who, int T, int H, int I, int E, int top_k) {
+  JANUS_REQUIRE(T >= 0 && H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0 && E > 0 && E <= kMaxExperts && top_k > 0 &&
+                    top_k <= E && (long)T * top_k < (1l << 30),
+                JANUS_MOE_EINVAL,
+                "%s: unsupported sizes T=%d H=%d I=%d E=%d top_k=%d (need H %% 128 == 0, I %% 128 == 0, E <= %d, "
+                "top_k <= E)", who, T, H, I, E, top_k, kMaxExperts);
+  return JANUS_MOE_OK;
+}
+
+// Runs align + the two grouped GEMMs + finalize; routing (idx, weights) already on the device.
+template <typename IdxT>
+int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const int32_t* guq, const uint16_t* gus,
+                const int32_t* dq, const uint16_t* ds, const int32_t* sguq, const uint16_t* sgus, const int32_t* sdq,
+                const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
+                const ExpertsWorkspace& w, hipStream_t stream) {
+  const int A = T * top_k;
+  int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
+                                   kChunkRows, w.num_chunks, w.acc, (long)T * H, stream);
+  if (rc) return rc;
+  const bool shared = I_s > 0;
+  GemmParams p = {};
+  p.sorted_ids = w.sorted_ids;
+  p.topk = top_k;
+  p.A = A;
+  p.T = T;
+  p.chunks = w.chunks;
+  p.num_chunks = w.num_chunks;
+  p.max_chunks = w.C;
+  p.n_shared_chunks = shared ? ceil_div(T, kChunkRows) : 0;
+  // gate_up
+  p.a = x;
+  p.q = guq;
+  p.s = gus;
+  p.N = 2 * I;
+  p.K = H;
+  p.q_sh = sguq;
+  p.s_sh = sgus;
+  p.N_sh = 2 * I_s;
+  p.K_sh = H;
+  p.nslab = ceil_div(I > I_s ? I : I_s, 128);
+  p.h = w.h;
+  p.h_sh = w.h_sh;
+  rc = launch_gate_up(p, stream);
+  if (rc) return rc;
+  // down + combine
+  p.a = w.h;
+  p.a_sh = w.h_sh;
+  p.q = dq;
+  p.s = ds;
+  p.N = H;
+  p.K = I;
+  p.q_sh = sdq;
+  p.s_sh = sds;
+  p.N_sh = H;
+  p.K_sh = I_s;
+  p.nslab = ceil_div(H, 256);
+  p.acc = w.acc;
+  p.route_w = route_w;
+  p.gamma = gamma;
+  rc = launch_down(p, stream);
+  if (rc) return rc;
+  return launch_finalize(w.acc, out, (long)T * H, stream);
+}
+
+struct BlockWorkspace {
+  RouteWorkspace route;
+  int32_t* topk_idx;
+  float* topk_w;
+  float* gamma;
+  ExpertsWorkspace experts;
+};
+
+BlockWorkspace carve_block(Carver& c, int T, int H, int I, int E, int top_k, int I_s) {
+  BlockWorkspace b;
+  b.route = carve_route(c, T, H, E);
+  b.topk_idx = c.take<int32_t>((size_t)T * top_k);
+  b.topk_w = c.take<float>((size_t)T * top_k);
+  b.gamma = c.take<float>(T);
+  b.experts = carve_experts(c, T, top_k, E, H, I, I_s);
+  return b;
+}
+
+}  // namespace
+}  // namespace janus
+
+using namespace janus;
+
+extern "C" const char* janus_moe_last_error(void) { return g_error; }
+extern "C" int janus_moe_abi_version(void) { return 1; }
+
+extern "C" size_t janus_moe_experts_workspace_bytes(int S, int top_k, int E, int H, int I) {
+  if (S < 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
+  Carver c(nullptr);
+  carve_experts(c, S, top_k, E, H, I, 0);
+  return align_up(c.used, 256);
+}
+
+extern "C" int janus_moe_experts(const uint16_t* x, const int64_t* top_k_index, const float* top_k_weights,
+                                 const int32_t* gate_up_q, const uint16_t* gate_up_s, const int32_t* down_q,
+                                 const uint16_t* down_s, int S, int H, int I, int E, int top_k, uint16_t* out, void* ws,
+                                 size_t ws_bytes, janus_stream_t stream) {
+  int rc = check_expert_sizes("janus_moe_experts", S, H, I, E, top_k);
+  if (rc) return rc;
+  if (S == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(x && top_k_index && top_k_weights && gate_up_q && gate_up_s && down_q && down_s && out,
+                JANUS_MOE_EINVAL, "janus_moe_experts: null pointer");
+  const size_t need = janus_moe_experts_workspace_bytes(S, top_k, E, H, I);
+  JANUS_REQUIRE(ws && ws_bytes >= need, JANUS_MOE_EWORKSPACE, "janus_moe_experts: workspace %zu < %zu bytes", ws_bytes,
+                need);
+  Carver c(ws);
+  ExpertsWorkspace w = carve_experts(c, S, top_k, E, H, I, 0);
+  return run_experts<int64_t>(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s, nullptr, nullptr,
+                              nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w, (hipStream_t)stream);
+}
+
+extern "C" size_t janus_moe_block_workspace_bytes(int T, int H, int I, int E, int top_k, int I_s) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || top_k <= 0 || I_s < 0) return 0;
+  Carver c(nullptr);
+  carve_block(c, T, H, I, E, top_k, I_s);
+  return align_up(c.used, 256);
+}
+
+extern "C" int janus_moe_block_forward(const janus_moe_block_weights* wt, const uint16_t* x, int T, uint16_t* out,
+                                       int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes,
+                                       janus_stream_t stream) {
+  JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward: null weights");
+  const int H = wt->H, I = wt->I, E = wt->E, k = wt->top_k, I_s = wt->I_s;
+  int rc = check_expert_sizes("janus_moe_block_forward", T, H, I, E, k);
+  if (rc) return rc;
+  rc = check_route_sizes(T, H, E, k);
+  if (rc) return rc;
+  JANUS_REQUIRE(I_s >= 0 && I_s % 128 == 0, JANUS_MOE_EINVAL, "janus_moe_block_forward: I_s=%d must be a multiple of 128",
+                I_s);
+  if (T == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(x && out && wt->router_w && wt->router_prep && wt->gate_up_q && wt->gate_up_s && wt->down_q &&
+                    wt->down_s && (I_s == 0 || (wt->sh_gate_up_q && wt->sh_gate_up_s && wt->sh_down_q && wt->sh_down_s)),
+                JANUS_MOE_EINVAL, "janus_moe_block_forward: null pointer");
+  const size_t need = janus_moe_block_workspace_bytes(T, H, I, E, k, I_s);
+  JANUS_REQUIRE(ws && ws_bytes >= need, JANUS_MOE_EWORKSPACE, "janus_moe_block_forward: workspace %zu < %zu bytes",
+                ws_bytes, need);
+  Carver c(ws);
+  BlockWorkspace b = carve_block(c, T, H, I, E, k, I_s);
+  int32_t* idx = topk_idx ? topk_idx : b.topk_idx;
+  float* rw = topk_w ? topk_w : b.topk_w;
+  const bool gated = I_s > 0 && wt->sh_gate_w;
+  rc = launch_route(x, wt->router_w, wt->router_prep, wt->router_bias, gated ? wt->sh_gate_w : nullptr, T, H, E, k, idx,
+                    rw, b.gamma, b.route, (hipStream_t)stream);
+  if (rc) return rc;
+  return run_experts<int>(x, idx, rw, wt->gate_up_q, wt->gate_up_s, wt->down_q, wt->down_s, wt->sh_gate_up_q,
+                          wt->sh_gate_up_s, wt->sh_down_q, wt->sh_down_s, gated ? b.gamma : nullptr, T, H, I, I_s, E, k,
+                          out, b.experts, (hipStream_t)stream);
+}
+
+extern "C" int janus_moe_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out,
+                                 janus_stream_t stream) {
+  JANUS_REQUIRE(rows >= 0 && K > 0 && K % 128 == 0, JANUS_MOE_EINVAL, "janus_moe_dequant: rows=%ld K=%d (need K %% 128 == 0)",
+                rows, K);
+  if (rows == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(q && s && out, JANUS_MOE_EINVAL, "janus_moe_dequant: null pointer");
+  return launch_dequant(q, s, rows, K, out, (hipStream_t)stream);
+}

@@ -1,0 +1,43 @@
+// Internal interface of the grouped W4A16 GEMM kernels (gemm.hip).
+#pragma once
+
+#include "common.h"
+
+namespace janus {
+
+constexpr int kChunkRows = 64;  // rows of one expert that one workgroup multiplies (4 MFMA row blocks)
+constexpr int kRowPad = 16;     // every expert's rows start at a multiple of this in the permuted order
+
+// One grouped GEMM launch over a chunk list (routed experts) plus, optionally, the shared expert as n_shared_chunks
+// chunks of consecutive tokens.
+//   gate_up: h[row, n] = bf16(silu(x[tok] . Wg[n]) * (x[tok] . Wu[n])) for n < I, W rows 0..I-1 gate, I..2I-1 up.
+//   down:    acc[tok, n] += w(row) * (h[row] . Wd[n]) in fp32 (atomic adds; acc cleared beforehand).
+struct GemmParams {
+  const uint16_t* a;          // gate_up: x [T, K]; down: h of the routed rows [P, K]
+  const uint16_t* a_sh;       // down: h of the shared expert [T, K_sh]
+  const int* sorted_ids;      // assignment id at each permuted position (< A on real rows)
+  int topk, A, T;
+  const int32_t* q;           // routed weight words [E, N, K/8]
+  const uint16_t* s;          // routed scales [E, N, K/128]
+  int N, K;                   // routed weight rows and reduction length
+  const int32_t* q_sh;        // shared expert [N_sh, K_sh/8], null = none
+  const uint16_t* s_sh;
+  int N_sh, K_sh;
+  const int4* chunks;         // (expert, first position, rows, 0)
+  const int* num_chunks;      // device count of valid chunks
+  int max_chunks;             // chunk list capacity (grid size)
+  int n_shared_chunks;        // ceil(T / kChunkRows) when the shared expert runs
+  int nslab;                  // column slabs per chunk
+  uint16_t* h;                // gate_up output, routed rows [P, N/2]
+  uint16_t* h_sh;             // gate_up output, shared rows [T, N_sh/2]
+  float* acc;                 // down output [T, N]
+  const float* route_w;       // down: routing weight per assignment id [A]
+  const float* gamma;         // down: shared-expert weight per token [T], null = 1
+};
+
+int launch_gate_up(const GemmParams& p, hipStream_t stream);
+int launch_down(const GemmParams& p, hipStream_t stream);
+int launch_finalize(const float* acc, uint16_t* out, long n, hipStream_t stream);
+int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream);
+
+}  // namespace janus

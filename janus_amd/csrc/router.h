@@ -1,0 +1,20 @@
+// Internal interface of the router kernels (router.hip).
+#pragma once
+
+#include "common.h"
+
+namespace janus {
+
+struct RouteWorkspace {
+  float* partial;  // [ceil(H/512), T, ceil(E/64)*64] approximate-logit partial sums
+};
+
+size_t router_prep_bytes(int E, int H);
+size_t route_workspace_bytes(int T, int H, int E);
+RouteWorkspace carve_route(Carver& c, int T, int H, int E);
+int check_route_sizes(int T, int H, int E, int top_k);
+int launch_route(const uint16_t* x, const float* w, const void* prep, const float* bias, const uint16_t* wsg, int T,
+                 int H, int E, int top_k, int32_t* topk_idx, float* topk_w, float* gamma, const RouteWorkspace& ws,
+                 hipStream_t stream);
+
+}  // namespace janus

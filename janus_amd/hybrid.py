@@ -1,0 +1,207 @@
+"""The MoE slice of janus/hybrid.py (:395-701) for the int4 group-128 codec: the codec, `W4A16Linear` (the
+NVFP4Linear counterpart), `W4A16Experts` (the NVFP4Experts counterpart, same forward signature and attributes) and
+`moe_kernel` (the JANUS_MOE_KERNEL switch).
+
+Dispatch follows janus/hybrid.py:551-572: under inference on a GPU the experts run the fused HIP kernels
+(`moe_w4a16.fused_moe`); with gradients enabled or on the CPU the stacks are dequantised per call and run through
+torch GEMMs (the reference's training and CPU paths: grouped, padded bmm or per-expert loop). Asking for `fused` on a
+CPU tensor raises, as the reference's Triton kernel would: nothing falls back silently from the HIP path.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+GROUP = 128
+BMM_CHUNK_TOKENS = 1024  # tokens per padded-bmm call, as janus/hybrid.py:396
+
+
+# ---- int4 group-128 codec ------------------------------------------------------------------------------------
+
+def int4_pack(codes: torch.Tensor) -> torch.Tensor:
+    """Signed codes [..., K] in [-8, 7] -> int32 words [..., K/8]; element 8j+i in bits 4i..4i+3 of word j."""
+    if codes.shape[-1] % 8:
+        raise ValueError("K must be a multiple of 8")
+    nib = (codes.to(torch.int64) & 0xF).reshape(*codes.shape[:-1], -1, 8)
+    shifts = torch.arange(0, 32, 4, device=codes.device, dtype=torch.int64)
+    words = (nib << shifts).sum(-1)
+    return torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
+
+
+def int4_unpack(words: torch.Tensor) -> torch.Tensor:
+    """int32 words [..., K/8] -> signed codes [..., K] int8."""
+    shifts = torch.arange(0, 32, 4, device=words.device, dtype=torch.int64)
+    nib = (words.to(torch.int64).unsqueeze(-1) >> shifts) & 0xF
+    return torch.where(nib >= 8, nib - 16, nib).to(torch.int8).flatten(-2)
+
+
+def int4_dequantize(words: torch.Tensor, scales: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """W = q * s, exact in fp32 (4-bit times 8-bit significands), rounded once to `dtype` (nearest even). bf16 on a
+    GPU runs the HIP decode kernel (janus_moe::dequant)."""
+    if words.is_cuda and dtype == torch.bfloat16:
+        from . import ops
+        return ops.dequant(words.contiguous(), scales.contiguous())
+    q = int4_unpack(words).float()
+    s = scales.float().repeat_interleave(GROUP, dim=-1)
+    return (q * s).to(dtype)
+
+
+def int4_quantize(w: torch.Tensor, group: int = GROUP) -> tuple[torch.Tensor, torch.Tensor]:
+    """A float weight [..., K] (K a multiple of `group`) to (int32 words [..., K/8], bf16 scales [..., K/group]):
+    symmetric, scale = bf16(amax / 7) per group (1 for an all-zero group), codes = clamp(round-half-even(w / s))."""
+    w = w.float()
+    blocks = w.reshape(*w.shape[:-1], -1, group)
+    s = (blocks.abs().amax(-1) / 7).to(torch.bfloat16)
+    s = torch.where(s == 0, torch.ones_like(s), s)
+    q = torch.clamp(torch.round(blocks / s.float()[..., None]), -8, 7).reshape(w.shape)
+    return int4_pack(q), s
+
+
+# ---- modules -------------------------------------------------------------------------------------------------
+
+def moe_kernel(device) -> str:
+    """`JANUS_MOE_KERNEL` (fused | grouped | bmm | loop) when set, else `fused` on a GPU and `bmm` on the CPU
+    (janus/hybrid.py:621-638). Any other value raises ValueError."""
+    choice = os.environ.get("JANUS_MOE_KERNEL", "").lower()
+    if choice in ("fused", "grouped", "bmm", "loop"):
+        return choice
+    if choice:
+        raise ValueError("JANUS_MOE_KERNEL must be fused, grouped, bmm or loop")
+    return "fused" if torch.device(device).type == "cuda" else "bmm"
+
+
+class W4A16Linear(nn.Module):
+    """A bias-free linear whose weight stays packed (int32 words [N, K/8], bf16 scales [N, K/128]; 0.52 bytes per
+    weight) and is dequantised at every call (janus/hybrid.py:483-509, the fp4=False mode). Buffers only."""
+
+    def __init__(self, words: torch.Tensor, scales: torch.Tensor):
+        super().__init__()
+        self.register_buffer("words", words, persistent=False)
+        self.register_buffer("scale", scales, persistent=False)
+        self.in_features, self.out_features = words.shape[1] * 8, words.shape[0]
+
+    def set_mode(self, fp4, fused=None):
+        if fp4:
+            raise ValueError("fp4 tensor-core mode needs NVFP4 weights; the int4 codec has none")
+
+    @property
+    def weight(self) -> torch.Tensor:
+        return int4_dequantize(self.words, self.scale, torch.bfloat16)
+
+    def forward(self, x):
+        return F.linear(x, self.weight.to(x.dtype))
+
+
+class W4A16Experts(nn.Module):
+    """The expert stack of a sparse MoE block (`gate_up_proj [E, 2I, H]`, `down_proj [E, H, I]`) held packed:
+    gate_up [E, 2I, H/8] int32 (rows 0..I-1 gate, I..2I-1 up), gate_up_scale [E, 2I, H/128] bf16, down [E, H, I/8],
+    down_scale [E, H, I/128]. The `*_global` buffers exist for fused_moe's reference arity (ones; the codec has no
+    global scale). forward has the HF experts' signature (janus/hybrid.py:512-618)."""
+
+    def __init__(self, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global, act_fn=F.silu):
+        super().__init__()
+        E = gate_up.shape[0]
+        if gate_up_global is None:
+            gate_up_global = torch.ones(E, gate_up.shape[1], 1, device=gate_up.device)
+        if down_global is None:
+            down_global = torch.ones(E, down.shape[1], 1, device=down.device)
+        for name, t in (("gate_up", gate_up), ("gate_up_scale", gate_up_scale), ("gate_up_global", gate_up_global),
+                        ("down", down), ("down_scale", down_scale), ("down_global", down_global)):
+            self.register_buffer(name, t, persistent=False)
+        self.num_experts, self.hidden_dim, self.intermediate_dim = E, gate_up.shape[2] * 8, down.shape[2] * 8
+        self.act_fn, self.has_gate, self.has_bias, self.is_transposed = act_fn, True, False, False
+        self.fused, self.blocked = None, None
+
+    def set_mode(self, fp4, fused=None):
+        if fp4:
+            raise ValueError("fp4 tensor-core mode needs NVFP4 weights; the int4 codec has none")
+        self.fused = fused
+
+    @property
+    def gate_up_proj(self) -> torch.Tensor:
+        return int4_dequantize(self.gate_up, self.gate_up_scale, torch.bfloat16)
+
+    @property
+    def down_proj(self) -> torch.Tensor:
+        return int4_dequantize(self.down, self.down_scale, torch.bfloat16)
+
+    def _apply_gate(self, gate_up_out):
+        gate, up = gate_up_out.chunk(2, dim=-1)
+        return self.act_fn(gate) * up
+
+    def forward(self, hidden_states, top_k_index, top_k_weights):
+        kernel = moe_kernel(hidden_states.device)
+        if (kernel == "fused" and not torch.is_grad_enabled() and self.hidden_dim % 128 == 0
+                and self.intermediate_dim % 128 == 0):
+            from .moe_w4a16 import fused_moe
+            return fused_moe(hidden_states, top_k_index, top_k_weights, self.gate_up, self.gate_up_scale,
+                             self.gate_up_global, self.down, self.down_scale, self.down_global)
+        if kernel == "fused":  # training or an unsupported shape: the dequantise paths, as the reference
+            kernel = "grouped" if hidden_states.is_cuda else "bmm"
+        if kernel == "grouped":
+            return self._grouped(hidden_states, top_k_index, top_k_weights, self.gate_up_proj, self.down_proj)
+        if kernel == "bmm":
+            gate_up, down = self.gate_up_proj, self.down_proj
+            return torch.cat([self._bmm(hidden_states[i:i + BMM_CHUNK_TOKENS], top_k_index[i:i + BMM_CHUNK_TOKENS],
+                                        top_k_weights[i:i + BMM_CHUNK_TOKENS], gate_up, down)
+                              for i in range(0, hidden_states.shape[0], BMM_CHUNK_TOKENS)])
+        return self._eager(hidden_states, top_k_index, top_k_weights, self.gate_up_proj, self.down_proj)
+
+    def _grouped(self, hidden_states, top_k_index, top_k_weights, gate_up, down):
+        """Assignments sorted by expert, one GEMM per expert on its contiguous slice, the weighted results put back in
+        assignment order and summed over the top-k in fp32 (transformers integrations/moe.py:377-476)."""
+        S, k = top_k_index.shape
+        flat = top_k_index.reshape(-1)
+        order = torch.argsort(flat, stable=True)
+        counts = torch.bincount(flat, minlength=self.num_experts).tolist()
+        x = hidden_states[order // k]
+        y = torch.empty(S * k, hidden_states.shape[1], dtype=x.dtype, device=x.device)
+        start = 0
+        for e, c in enumerate(counts):
+            if c:
+                h = self._apply_gate(F.linear(x[start:start + c], gate_up[e].to(x.dtype)))
+                y[start:start + c] = F.linear(h, down[e].to(x.dtype))
+            start += c
+        y = y * top_k_weights.reshape(-1)[order, None].to(y.dtype)
+        out = torch.empty_like(y)
+        out[order] = y
+        return out.view(S, k, -1).float().sum(1).to(hidden_states.dtype)
+
+    def _bmm(self, hidden_states, top_k_index, top_k_weights, gate_up, down):
+        """Every expert's tokens padded to the busiest expert's count, one bmm per projection, scatter-add
+        (janus/hybrid.py:574-598)."""
+        S, k = top_k_index.shape
+        flat = top_k_index.reshape(-1)
+        order = torch.argsort(flat, stable=True)
+        counts = torch.bincount(flat, minlength=self.num_experts)
+        starts = counts.cumsum(0) - counts
+        width = int(counts.max()) if counts.numel() else 0
+        slot = torch.arange(S * k, device=order.device) - starts[flat[order]]
+        index = torch.full((self.num_experts, width), S, dtype=torch.long, device=order.device)
+        index[flat[order], slot] = order // k
+        x = torch.cat([hidden_states, hidden_states.new_zeros(1, hidden_states.shape[1])])[index]
+        h = self._apply_gate(torch.bmm(x, gate_up.transpose(1, 2).to(x.dtype).contiguous()))
+        y = torch.bmm(h, down.transpose(1, 2).to(x.dtype).contiguous())
+        valid = index.reshape(-1) < S
+        weight = torch.zeros(self.num_experts * width, dtype=hidden_states.dtype, device=order.device)
+        weight[flat[order] * width + slot] = top_k_weights.reshape(-1)[order].to(hidden_states.dtype)
+        out = torch.zeros_like(hidden_states)
+        out.index_add_(0, index.reshape(-1)[valid], (y.reshape(-1, y.shape[-1]) * weight[:, None])[valid])
+        return out
+
+    def _eager(self, hidden_states, top_k_index, top_k_weights, gate_up, down):
+        """Per hit expert: gather its tokens, the two GEMMs, scatter-add (janus/hybrid.py:600-618)."""
+        out = torch.zeros_like(hidden_states)
+        hits = torch.bincount(top_k_index.flatten(), minlength=self.num_experts).tolist()
+        for e, count in enumerate(hits):
+            if count == 0:
+                continue
+            token, slot = torch.where(top_k_index == e)
+            x = hidden_states[token]
+            h = self._apply_gate(F.linear(x, gate_up[e].to(x.dtype)))
+            y = F.linear(h, down[e].to(x.dtype))
+            out.index_add_(0, token, (y * top_k_weights[token, slot, None]).to(out.dtype))
+        return out

@@ -1,0 +1,255 @@
+"""The C ABI registered as PyTorch custom ops (namespace `janus_moe`).
+
+Each op checks shapes and dtypes on the host, allocates its outputs and scratch with torch (so the caching allocator,
+or a graph's private pool under capture, owns them), and launches on the current stream of the input's device.
+Nothing reads device memory back: the ops are sync-free and capturable in a HIP graph. They run only on GPU tensors
+and raise otherwise; there is no CPU path behind them.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import check
+
+_ptr_t = ctypes.c_void_p
+
+
+def _ptr(t: Optional[Tensor]):
+    return None if t is None else _ptr_t(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return _ptr_t(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*tensors: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"janus_moe ops run on the GPU only (HIP kernels); got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"janus_moe ops: tensors on {dev} and {t.device}")
+    return dev
+
+
+def _expect(t: Tensor, name: str, dtype: torch.dtype, shape: tuple) -> None:
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected {dtype} {tuple(shape)}, got {t.dtype} {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+
+
+def _workspace(nbytes: int, device: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---- router --------------------------------------------------------------------------------------------------
+
+@torch.library.custom_op("janus_moe::router_prepare", mutates_args=())
+def router_prepare(w_router: Tensor) -> Tensor:
+    """Split of the fp32 router weight [E, H] the route op reads (bf16 planes and norms), as a byte buffer."""
+    dev = _require_gpu(w_router)
+    E, H = w_router.shape
+    _expect(w_router, "w_router", torch.float32, (E, H))
+    L = _lib.lib()
+    n = L.janus_moe_router_prep_bytes(E, H)
+    prep = torch.empty(n, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_router_prepare(_ptr(w_router), E, H, _ptr(prep), n, _stream(dev)), "janus_moe_router_prepare")
+    return prep
+
+
+@router_prepare.register_fake
+def _(w_router):
+    E, H = w_router.shape
+    return w_router.new_empty(_lib.lib().janus_moe_router_prep_bytes(E, H), dtype=torch.uint8)
+
+
+@torch.library.custom_op("janus_moe::route", mutates_args=())
+def route(x: Tensor, w_router: Tensor, prep: Tensor, bias: Optional[Tensor], w_shared_gate: Optional[Tensor],
+          top_k: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Top-k routing of x [T, H] bf16: (indices [T, k] int32, weights [T, k] fp32, sigmoid shared gate [T] fp32)."""
+    dev = _require_gpu(x, w_router, prep, bias, w_shared_gate)
+    T, H = x.shape
+    E = w_router.shape[0]
+    _expect(x, "x", torch.bfloat16, (T, H))
+    _expect(w_router, "w_router", torch.float32, (E, H))
+    if bias is not None:
+        _expect(bias, "bias", torch.float32, (E,))
+    if w_shared_gate is not None:
+        _expect(w_shared_gate, "w_shared_gate", torch.bfloat16, (H,))
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    gamma = torch.empty(T, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    n = L.janus_moe_route_workspace_bytes(T, H, E)
+    ws = _workspace(n, dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_route(_ptr(x), _ptr(w_router), _ptr(prep), _ptr(bias), _ptr(w_shared_gate), T, H, E, top_k,
+                                _ptr(idx), _ptr(w), _ptr(gamma), _ptr(ws), ws.numel(), _stream(dev)), "janus_moe_route")
+    return idx, w, gamma
+
+
+@route.register_fake
+def _(x, w_router, prep, bias, w_shared_gate, top_k):
+    T = x.shape[0]
+    return (x.new_empty(T, top_k, dtype=torch.int32), x.new_empty(T, top_k, dtype=torch.float32),
+            x.new_empty(T, dtype=torch.float32))
+
+
+# ---- dequantise ----------------------------------------------------------------------------------------------
+
+@torch.library.custom_op("janus_moe::dequant", mutates_args=())
+def dequant(words: Tensor, scales: Tensor) -> Tensor:
+    """int4 group-128 matrix or stack (words [..., K/8] int32, scales [..., K/128] bf16) -> bf16 [..., K] =
+    bf16(q * s), by the decode the GEMMs use."""
+    dev = _require_gpu(words, scales)
+    K = words.shape[-1] * 8
+    rows = words.numel() // max(words.shape[-1], 1)
+    _expect(words, "words", torch.int32, tuple(words.shape))
+    _expect(scales, "scales", torch.bfloat16, (*words.shape[:-1], K // 128))
+    out = torch.empty(*words.shape[:-1], K, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().janus_moe_dequant(_ptr(words), _ptr(scales), rows, K, _ptr(out), _stream(dev)),
+              "janus_moe_dequant")
+    return out
+
+
+@dequant.register_fake
+def _(words, scales):
+    return words.new_empty(*words.shape[:-1], words.shape[-1] * 8, dtype=torch.bfloat16)
+
+
+# ---- align ---------------------------------------------------------------------------------------------------
+
+def align_shapes(S: int, k: int, num_experts: int, block: int) -> int:
+    return (S * k + num_experts * (block - 1) + block - 1) // block
+
+
+@torch.library.custom_op("janus_moe::align", mutates_args=())
+def align(top_k_index: Tensor, num_experts: int, block: int) -> tuple[Tensor, Tensor, Tensor]:
+    """(sorted_ids [tiles*block] int64, expert_ids [tiles] int64, total [1] int64) as janus/moe_w4a16.py:89-106."""
+    dev = _require_gpu(top_k_index)
+    S, k = top_k_index.shape
+    _expect(top_k_index, "top_k_index", torch.int64, (S, k))
+    tiles = align_shapes(S, k, num_experts, block)
+    sorted_ids = torch.empty(tiles * block, dtype=torch.int64, device=dev)
+    expert_ids = torch.empty(tiles, dtype=torch.int64, device=dev)
+    total = torch.empty(1, dtype=torch.int64, device=dev)
+    L = _lib.lib()
+    n = L.janus_moe_align_workspace_bytes(S, k, num_experts)
+    ws = _workspace(n, dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_align(_ptr(top_k_index), S, k, num_experts, block, _ptr(sorted_ids), _ptr(expert_ids),
+                                _ptr(total), _ptr(ws), ws.numel(), _stream(dev)), "janus_moe_align")
+    return sorted_ids, expert_ids, total
+
+
+@align.register_fake
+def _(top_k_index, num_experts, block):
+    S, k = top_k_index.shape
+    tiles = align_shapes(S, k, num_experts, block)
+    return (top_k_index.new_empty(tiles * block), top_k_index.new_empty(tiles), top_k_index.new_empty(1))
+
+
+# ---- routed experts ------------------------------------------------------------------------------------------
+
+def _expert_shapes(gate_up_q: Tensor, down_q: Tensor) -> tuple[int, int, int]:
+    E, two_i, h8 = gate_up_q.shape
+    return E, h8 * 8, two_i // 2
+
+
+@torch.library.custom_op("janus_moe::experts", mutates_args=())
+def experts(x: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_q: Tensor, gate_up_s: Tensor,
+            down_q: Tensor, down_s: Tensor) -> Tensor:
+    """Routed W4A16 experts with the fp32 weighted combine: [S, H] bf16."""
+    dev = _require_gpu(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s)
+    S, H = x.shape
+    k = top_k_index.shape[1]
+    E, Hw, I = _expert_shapes(gate_up_q, down_q)
+    if Hw != H:
+        raise ValueError(f"gate_up_q packs K={Hw}, x has H={H}")
+    _expect(x, "x", torch.bfloat16, (S, H))
+    _expect(top_k_index, "top_k_index", torch.int64, (S, k))
+    _expect(top_k_weights, "top_k_weights", torch.float32, (S, k))
+    _expect(gate_up_q, "gate_up_q", torch.int32, (E, 2 * I, H // 8))
+    _expect(gate_up_s, "gate_up_s", torch.bfloat16, (E, 2 * I, H // 128))
+    _expect(down_q, "down_q", torch.int32, (E, H, I // 8))
+    _expect(down_s, "down_s", torch.bfloat16, (E, H, I // 128))
+    out = torch.empty(S, H, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    n = L.janus_moe_experts_workspace_bytes(S, k, E, H, I)
+    ws = _workspace(n, dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_experts(_ptr(x), _ptr(top_k_index), _ptr(top_k_weights), _ptr(gate_up_q), _ptr(gate_up_s),
+                                  _ptr(down_q), _ptr(down_s), S, H, I, E, k, _ptr(out), _ptr(ws), ws.numel(),
+                                  _stream(dev)), "janus_moe_experts")
+    return out
+
+
+@experts.register_fake
+def _(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s):
+    return torch.empty_like(x)
+
+
+# ---- whole block ---------------------------------------------------------------------------------------------
+
+@torch.library.custom_op("janus_moe::block_forward", mutates_args=())
+def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias: Optional[Tensor], gate_up_q: Tensor,
+                  gate_up_s: Tensor, down_q: Tensor, down_s: Tensor, sh_gate_up_q: Optional[Tensor],
+                  sh_gate_up_s: Optional[Tensor], sh_down_q: Optional[Tensor], sh_down_s: Optional[Tensor],
+                  sh_gate_w: Optional[Tensor], top_k: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Router + routed experts + gated shared expert, one fp32 sum rounded once: (out [T, H] bf16, indices [T, k]
+    int32, weights [T, k] fp32)."""
+    dev = _require_gpu(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s, sh_gate_up_q,
+                       sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w)
+    T, H = x.shape
+    E, Hw, I = _expert_shapes(gate_up_q, down_q)
+    if Hw != H:
+        raise ValueError(f"gate_up_q packs K={Hw}, x has H={H}")
+    _expect(x, "x", torch.bfloat16, (T, H))
+    _expect(router_w, "router_w", torch.float32, (E, H))
+    _expect(gate_up_q, "gate_up_q", torch.int32, (E, 2 * I, H // 8))
+    _expect(gate_up_s, "gate_up_s", torch.bfloat16, (E, 2 * I, H // 128))
+    _expect(down_q, "down_q", torch.int32, (E, H, I // 8))
+    _expect(down_s, "down_s", torch.bfloat16, (E, H, I // 128))
+    if router_bias is not None:
+        _expect(router_bias, "router_bias", torch.float32, (E,))
+    I_s = 0
+    if sh_gate_up_q is not None:
+        I_s = sh_gate_up_q.shape[0] // 2
+        _expect(sh_gate_up_q, "sh_gate_up_q", torch.int32, (2 * I_s, H // 8))
+        _expect(sh_gate_up_s, "sh_gate_up_s", torch.bfloat16, (2 * I_s, H // 128))
+        _expect(sh_down_q, "sh_down_q", torch.int32, (H, I_s // 8))
+        _expect(sh_down_s, "sh_down_s", torch.bfloat16, (H, I_s // 128))
+        if sh_gate_w is not None:
+            _expect(sh_gate_w, "sh_gate_w", torch.bfloat16, (H,))
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    rw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    weights = _lib.BlockWeights(H, I, E, top_k, I_s, *[_ptr(t) for t in (
+        router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s,
+        sh_gate_up_q, sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w)])
+    L = _lib.lib()
+    n = L.janus_moe_block_workspace_bytes(T, H, I, E, top_k, I_s)
+    ws = _workspace(n, dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_block_forward(ctypes.byref(weights), _ptr(x), T, _ptr(out), _ptr(idx), _ptr(rw), _ptr(ws),
+                                        ws.numel(), _stream(dev)), "janus_moe_block_forward")
+    return out, idx, rw
+
+
+@block_forward.register_fake
+def _(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s, sh_gate_up_q, sh_gate_up_s,
+      sh_down_q, sh_down_s, sh_gate_w, top_k):
+    T = x.shape[0]
+    return (torch.empty_like(x), x.new_empty(T, top_k, dtype=torch.int32), x.new_empty(T, top_k, dtype=torch.float32))

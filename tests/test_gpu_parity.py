@@ -1,0 +1,180 @@
+"""Parity of the HIP path (through the C ABI, via the janus_moe custom ops) with the CPU oracle, on the GPU.
+
+Bars: routing indices, align plans and the int4 decode bit-exact; layer outputs within the tolerance the reference's
+own fused-kernel test uses (tests/test_hybrid.py:745-746: assert_close atol = rtol = 2e-2 and max|d| <= 0.02 max|ref|
++ 1e-3) plus relative L2 <= 1e-3; routing weights within 1e-4 relative.
+"""
+import numpy as np
+import pytest
+import torch
+
+from janus_amd import ops, synth
+from janus_amd.block import W4A16SparseMoeBlock
+from janus_amd.moe_w4a16 import align, fused_moe
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+
+
+def assert_layer_close(out: np.ndarray, ref: np.ndarray, what: str):
+    """The reference test's form (tests/test_hybrid.py:745-746) plus relative L2."""
+    out = np.asarray(out, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    d = np.abs(out - ref)
+    rel_l2 = np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30)
+    torch.testing.assert_close(torch.from_numpy(out), torch.from_numpy(ref), atol=2e-2, rtol=2e-2, msg=what)
+    assert d.max() <= 0.02 * np.abs(ref).max() + 1e-3, (what, d.max(), np.abs(ref).max())
+    assert rel_l2 <= REL_L2, (what, rel_l2)
+    return rel_l2
+
+
+def bf16_np(t: torch.Tensor) -> np.ndarray:
+    return O.bf16_values(t)
+
+
+# ---- decode ----------------------------------------------------------------------------------------------------
+
+def test_dequant_bit_exact_over_codes_and_scales(gpu):
+    """Every 4-bit code times every positive and negative bf16 scale with exponent in [-100, 100]: the HIP decode
+    equals RNE_bf16(q * s)."""
+    exps = np.arange(-100, 101)
+    mant = np.arange(128)
+    sbits = ((exps[:, None] + 127) << 7 | mant[None, :]).reshape(-1).astype(np.uint16)
+    sbits = np.concatenate([sbits, sbits | 0x8000])
+    rows = sbits.size
+    codes = np.tile(np.arange(-8, 8), 8)                      # 128 values, each code 8 times
+    nib = (codes & 0xF).astype(np.uint32).reshape(16, 8)
+    words = np.zeros(16, dtype=np.uint32)
+    for i in range(8):
+        words |= nib[:, i] << np.uint32(4 * i)
+    q = np.broadcast_to(words.view(np.int32), (rows, 16)).copy()
+    s = sbits.reshape(rows, 1)
+    got = ops.dequant(torch.from_numpy(q).to(gpu), torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).to(gpu))
+    got_bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
+    want_bits = O.bf16_to_bits(O.dequant(q, s))
+    assert np.array_equal(got_bits, want_bits), np.argwhere(got_bits != want_bits)[:5]
+
+
+# ---- align -----------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("S,k,E,block,skew", [
+    (0, 2, 8, 16, 0), (1, 1, 1, 16, 0), (5, 2, 8, 16, 0), (40, 2, 8, 16, 1), (96, 8, 256, 16, 0),
+    (700, 8, 16, 64, 1), (2048, 8, 256, 64, 0), (2048, 8, 256, 16, 2), (3000, 4, 60, 32, 0),
+    (16384, 8, 256, 64, 0), (16384, 8, 256, 128, 2), (1000, 8, 1024, 16, 0),
+])
+def test_align_bit_exact(gpu, S, k, E, block, skew):
+    rng = np.random.default_rng(S * 31 + E)
+    idx = rng.integers(0, E, size=(S, k))
+    if skew == 1 and S:
+        idx[: S // 2, 0] = min(2, E - 1)          # a hot expert spanning several tiles
+    if skew == 2 and S:
+        idx = np.minimum(rng.zipf(1.3, size=(S, k)) - 1, E - 1)
+    got = align(torch.from_numpy(idx).to(gpu), E, block)
+    want = O.align(idx, E, block)
+    for g, w, name in zip(got, want, ("sorted_ids", "expert_ids", "total")):
+        assert np.array_equal(g.cpu().numpy(), w), name
+
+
+def test_align_single_expert_known_answer(gpu):
+    """tests/test_hybrid.py:720-721: align(full((5, 2), 7), 8, 16).total == 16."""
+    _, _, total = align(torch.full((5, 2), 7, device=gpu), 8, 16)
+    assert int(total) == 16
+
+
+# ---- router ----------------------------------------------------------------------------------------------------
+
+def _route_case(cfg, gpu, seed=17, tokens=None):
+    L = synth.layer(cfg, seed)
+    x = synth.activations(cfg, seed, tokens)
+    prep = ops.router_prepare(L["router_w"].to(gpu))
+    bias = None if L["router_bias"] is None else L["router_bias"].to(gpu)
+    idx, w, _ = ops.route(x.to(gpu), L["router_w"].to(gpu), prep, bias, None, cfg.k)
+    ridx, rw, _ = O.route(bf16_np(x), L["router_w"].numpy(), cfg.k,
+                          None if L["router_bias"] is None else L["router_bias"].numpy())
+    return idx.cpu().numpy(), w.cpu().numpy(), ridx, rw
+
+
+@pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf"])
+def test_route_bit_exact(gpu, name):
+    cfg = synth.CONFIGS[name]
+    idx, w, ridx, rw = _route_case(cfg, gpu)
+    assert np.array_equal(idx, ridx), np.argwhere(idx != ridx)[:5]
+    np.testing.assert_allclose(w, rw, rtol=1e-4, atol=1e-6)
+
+
+def test_route_ties_go_to_the_lower_expert(gpu):
+    """Duplicated router rows give exactly equal logits: the lower expert id takes the earlier slot."""
+    E, H, k, T = 32, 512, 4, 64
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(E, H, generator=g) * 0.02
+    w[9] = w[3]
+    w[20] = w[3]
+    w[31] = w[30]
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    x[: T // 2] = (x[: T // 2].float() + 8 * torch.from_numpy(np.asarray(w[3].numpy() / 0.02)).float()).bfloat16()
+    prep = ops.router_prepare(w.to(gpu))
+    idx, rw, _ = ops.route(x.to(gpu), w.to(gpu), prep, None, None, k)
+    ridx, rrw, _ = O.route(bf16_np(x), w.numpy(), k)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(rw.cpu().numpy(), rrw, rtol=1e-4, atol=1e-6)
+    # the first half of the tokens favour expert 3 and its copies 9 and 20: they appear in id order
+    first = ridx[: T // 2]
+    for row in first:
+        pos = [list(row).index(e) for e in (3, 9, 20) if e in row]
+        assert pos == sorted(pos)
+
+
+# ---- experts (fused_moe) ---------------------------------------------------------------------------------------
+
+def _experts_case(gpu, S, E, H, I, k, seed, hot=True, unused_last=True):
+    rng = np.random.default_rng(seed)
+    cfg = synth.LayerConfig("case", T=S, H=H, E=E, k=k, I=I)
+    L = synth.layer(cfg, seed)
+    x = synth.activations(cfg, seed)
+    idx = rng.integers(0, E - 1 if unused_last else E, size=(S, k))
+    if hot:
+        idx[: S // 2, 0] = 2
+    w = torch.softmax(torch.from_numpy(rng.standard_normal((S, k))), -1).float()
+    out = fused_moe(x.to(gpu), torch.from_numpy(idx).to(gpu), w.to(gpu), L["gate_up_q"].to(gpu),
+                    L["gate_up_s"].to(gpu), None, L["down_q"].to(gpu), L["down_s"].to(gpu), None)
+    n = O.numpy_layer(L)
+    ref = O.bf16_round(O.expert_sum(bf16_np(x), idx, w.numpy(), n["gate_up_q"], n["gate_up_s"], n["down_q"],
+                                    n["down_s"]))
+    return bf16_np(out), ref
+
+
+@pytest.mark.parametrize("S", [3, 100, 700])
+def test_fused_moe_matches_oracle_reference_test_shapes(gpu, S):
+    """tests/test_hybrid.py:725-746's case: E=16, I=512, H=2048, top-8, a hot expert on half the tokens, the last
+    expert never hit."""
+    out, ref = _experts_case(gpu, S, 16, 2048, 512, 8, seed=S)
+    assert_layer_close(out, ref, f"S={S}")
+
+
+def test_fused_moe_tiny(gpu):
+    out, ref = _experts_case(gpu, 128, 16, 512, 256, 2, seed=5, hot=False, unused_last=False)
+    assert_layer_close(out, ref, "tiny")
+
+
+# ---- whole block -----------------------------------------------------------------------------------------------
+
+def _block(cfg, gpu, seed=17):
+    L = synth.layer(cfg, seed)
+    blk = W4A16SparseMoeBlock.from_tensors(L, cfg.k).to(gpu)
+    return L, blk
+
+
+@pytest.mark.parametrize("name,sample", [("tiny", None), ("short", None), ("headline", 48), ("zipf", 48)])
+def test_block_matches_oracle(gpu, name, sample):
+    cfg = synth.CONFIGS[name]
+    L, blk = _block(cfg, gpu)
+    x = synth.activations(cfg)
+    with torch.no_grad():
+        out = blk(x.to(gpu))
+    torch.cuda.synchronize()
+    tokens = None if sample is None else np.linspace(0, cfg.T - 1, sample).astype(int)
+    ref, _, _, _ = O.block_forward(O.numpy_layer(L), bf16_np(x), cfg.k, tokens)
+    got = bf16_np(out) if tokens is None else bf16_np(out)[tokens]
+    assert_layer_close(got, ref, name)
