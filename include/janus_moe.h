@@ -45,6 +45,12 @@ JANUS_MOE_API const char* janus_moe_last_error(void);
 /* Bumped whenever a signature below changes. */
 JANUS_MOE_API int janus_moe_abi_version(void);
 
+/* Profiling hook with no counterpart in the reference: while set (count > 0), the experts and block pipelines of the
+ * calling thread record events[i] (hipEvent_t) on their stream at stage boundaries: 0 start, 1 before align,
+ * 2 before the gate_up GEMM, 3 before the down GEMM, 4 before the combine, 5 end. count = 0 turns it off. The events
+ * belong to the caller; at most 6. */
+JANUS_MOE_API int janus_moe_profile_events(void* const* events, int count);
+
 /* ------------------------------------------------------------------------------------------------------------
  * Router.
  * janus_moe_router_prepare has no counterpart in the reference: it splits the fp32 router weight [E, H] once

@@ -20,7 +20,7 @@ EXPORTS = (
     "janus_moe_align_workspace_bytes", "janus_moe_align",
     "janus_moe_experts_workspace_bytes", "janus_moe_experts",
     "janus_moe_block_workspace_bytes", "janus_moe_block_forward",
-    "janus_moe_dequant",
+    "janus_moe_dequant", "janus_moe_profile_events",
 )
 
 _p, _i, _z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -51,6 +51,7 @@ _SIGNATURES = {
     "janus_moe_block_workspace_bytes": (_z, [_i, _i, _i, _i, _i, _i]),
     "janus_moe_block_forward": (_i, [ctypes.POINTER(BlockWeights), _p, _i, _p, _p, _p, _p, _z, _p]),
     "janus_moe_dequant": (_i, [_p, _p, ctypes.c_long, _i, _p, _p]),
+    "janus_moe_profile_events": (_i, [ctypes.POINTER(_p), _i]),
 }
 
 _handle = None

@@ -1,8 +1,8 @@
 // Pipelines behind the experts and block entry points, workspace layouts, and the error channel.
 //
-// experts (fused_moe, janus/moe_w4a16.py:122-140):   align -> gate_up -> down (+ combine) -> finalize
+// experts (fused_moe, janus/moe_w4a16.py:122-140):   align -> gate_up -> down (weighted slots) -> combine
 // block   (Qwen3_5MoeSparseMoeBlock.forward):        route -> align -> gate_up (+ shared) -> down (+ shared, combine)
-//                                                     -> finalize
+//                                                     -> combine (fp32 slot sum, one rounding)
 // Every launch goes on the caller's stream; counts stay on the device (grids are sized for the worst case and idle
 // workgroups exit), so a caller can capture the whole sequence in a HIP graph.
 #include <stdarg.h>
@@ -15,6 +15,15 @@ namespace janus {
 
 namespace {
 thread_local char g_error[512] = "";
+constexpr int kStageEvents = 6;
+thread_local hipEvent_t g_events[kStageEvents] = {};
+thread_local int g_nevents = 0;
+
+// Stage boundaries of the pipelines: 0 start (before route), 1 before align, 2 before gate_up, 3 before down,
+// 4 before the combine, 5 end.
+void mark(int i, hipStream_t stream) {
+  if (i < g_nevents && g_events[i]) (void)hipEventRecord(g_events[i], stream);
+}
 }
 
 void set_error(const char* fmt, ...) {
@@ -33,8 +42,8 @@ struct ExpertsWorkspace {
   int* num_chunks;  // [1]
   uint16_t* h;      // [P, I]
   uint16_t* h_sh;   // [T, I_s]
-  float* acc;       // [T, H]
-  int P, C;
+  float* slots;     // [T, nslots, H] weighted expert outputs
+  int P, C, nslots;
 };
 
 ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I, int I_s) {
@@ -48,7 +57,8 @@ ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I,
   w.num_chunks = c.take<int>(1);
   w.h = c.take<uint16_t>((size_t)w.P * I);
   w.h_sh = c.take<uint16_t>((size_t)T * I_s);
-  w.acc = c.take<float>((size_t)T * H);
+  w.nslots = top_k + (I_s > 0 ? 1 : 0);
+  w.slots = c.take<float>((size_t)T * w.nslots * H);
   return w;
 }
 
@@ -61,15 +71,16 @@ int check_expert_sizes(const char* who, int T, int H, int I, int E, int top_k) {
   return JANUS_MOE_OK;
 }
 
-// Runs align + the two grouped GEMMs + finalize; routing (idx, weights) already on the device.
+// Runs align + the two grouped GEMMs + the combine; routing (idx, weights) already on the device.
 template <typename IdxT>
 int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const int32_t* guq, const uint16_t* gus,
                 const int32_t* dq, const uint16_t* ds, const int32_t* sguq, const uint16_t* sgus, const int32_t* sdq,
                 const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
                 const ExpertsWorkspace& w, hipStream_t stream) {
   const int A = T * top_k;
+  mark(1, stream);
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
-                                   kChunkRows, w.num_chunks, w.acc, (long)T * H, stream);
+                                   kChunkRows, w.num_chunks, nullptr, 0, stream);
   if (rc) return rc;
   const bool shared = I_s > 0;
   GemmParams p = {};
@@ -94,9 +105,10 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.nslab = ceil_div(I > I_s ? I : I_s, 128);
   p.h = w.h;
   p.h_sh = w.h_sh;
+  mark(2, stream);
   rc = launch_gate_up(p, stream);
   if (rc) return rc;
-  // down + combine
+  // down: weighted expert outputs into the slots
   p.a = w.h;
   p.a_sh = w.h_sh;
   p.q = dq;
@@ -108,12 +120,17 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.N_sh = H;
   p.K_sh = I_s;
   p.nslab = ceil_div(H, 256);
-  p.acc = w.acc;
+  p.slots = w.slots;
+  p.nslots = w.nslots;
   p.route_w = route_w;
   p.gamma = gamma;
+  mark(3, stream);
   rc = launch_down(p, stream);
   if (rc) return rc;
-  return launch_finalize(w.acc, out, (long)T * H, stream);
+  mark(4, stream);
+  rc = launch_combine(w.slots, w.nslots, out, T, H, stream);
+  mark(5, stream);
+  return rc;
 }
 
 struct BlockWorkspace {
@@ -142,6 +159,14 @@ using namespace janus;
 extern "C" const char* janus_moe_last_error(void) { return g_error; }
 extern "C" int janus_moe_abi_version(void) { return 1; }
 
+extern "C" int janus_moe_profile_events(void* const* events, int count) {
+  JANUS_REQUIRE(count >= 0 && count <= kStageEvents && (count == 0 || events), JANUS_MOE_EINVAL,
+                "janus_moe_profile_events: count=%d (at most %d)", count, kStageEvents);
+  for (int i = 0; i < kStageEvents; ++i) g_events[i] = i < count ? static_cast<hipEvent_t>(events[i]) : nullptr;
+  g_nevents = count;
+  return JANUS_MOE_OK;
+}
+
 extern "C" size_t janus_moe_experts_workspace_bytes(int S, int top_k, int E, int H, int I) {
   if (S < 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
   Carver c(nullptr);
@@ -163,6 +188,7 @@ extern "C" int janus_moe_experts(const uint16_t* x, const int64_t* top_k_index, 
                 need);
   Carver c(ws);
   ExpertsWorkspace w = carve_experts(c, S, top_k, E, H, I, 0);
+  mark(0, (hipStream_t)stream);
   return run_experts<int64_t>(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s, nullptr, nullptr,
                               nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w, (hipStream_t)stream);
 }
@@ -197,6 +223,7 @@ extern "C" int janus_moe_block_forward(const janus_moe_block_weights* wt, const 
   int32_t* idx = topk_idx ? topk_idx : b.topk_idx;
   float* rw = topk_w ? topk_w : b.topk_w;
   const bool gated = I_s > 0 && wt->sh_gate_w;
+  mark(0, (hipStream_t)stream);
   rc = launch_route(x, wt->router_w, wt->router_prep, wt->router_bias, gated ? wt->sh_gate_w : nullptr, T, H, E, k, idx,
                     rw, b.gamma, b.route, (hipStream_t)stream);
   if (rc) return rc;

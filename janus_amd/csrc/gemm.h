@@ -5,13 +5,15 @@
 
 namespace janus {
 
-constexpr int kChunkRows = 64;  // rows of one expert that one workgroup multiplies (4 MFMA row blocks)
-constexpr int kRowPad = 16;     // every expert's rows start at a multiple of this in the permuted order
+constexpr int kRowBlocks = 6;                 // MFMA row blocks per workgroup tile
+constexpr int kChunkRows = 16 * kRowBlocks;   // rows of one expert (or shared-expert tokens) per workgroup
+constexpr int kRowPad = 16;                   // every expert's rows start at a multiple of this in the permuted order
 
 // One grouped GEMM launch over a chunk list (routed experts) plus, optionally, the shared expert as n_shared_chunks
 // chunks of consecutive tokens.
 //   gate_up: h[row, n] = bf16(silu(x[tok] . Wg[n]) * (x[tok] . Wu[n])) for n < I, W rows 0..I-1 gate, I..2I-1 up.
-//   down:    acc[tok, n] += w(row) * (h[row] . Wd[n]) in fp32 (atomic adds; acc cleared beforehand).
+//   down:    slots[tok, slot, n] = w(row) * (h[row] . Wd[n]) in fp32, slot = the assignment's top-k slot, or top_k for
+//            the shared expert (weight sigmoid gate). A combine pass sums the slots of each token.
 struct GemmParams {
   const uint16_t* a;          // gate_up: x [T, K]; down: h of the routed rows [P, K]
   const uint16_t* a_sh;       // down: h of the shared expert [T, K_sh]
@@ -30,14 +32,16 @@ struct GemmParams {
   int nslab;                  // column slabs per chunk
   uint16_t* h;                // gate_up output, routed rows [P, N/2]
   uint16_t* h_sh;             // gate_up output, shared rows [T, N_sh/2]
-  float* acc;                 // down output [T, N]
+  float* slots;               // down output [T, nslots, N]
+  int nslots;                 // top_k, plus one when the shared expert runs
   const float* route_w;       // down: routing weight per assignment id [A]
   const float* gamma;         // down: shared-expert weight per token [T], null = 1
 };
 
 int launch_gate_up(const GemmParams& p, hipStream_t stream);
 int launch_down(const GemmParams& p, hipStream_t stream);
-int launch_finalize(const float* acc, uint16_t* out, long n, hipStream_t stream);
+// out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32.
+int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, hipStream_t stream);
 int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream);
 
 }  // namespace janus

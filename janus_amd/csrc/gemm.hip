@@ -1,17 +1,20 @@
 // Grouped W4A16 GEMMs for gfx950: int4 group-128 weights decoded to bf16 in registers, bf16 MFMA with fp32
-// accumulation. The semantics are those of the reference's per-tile kernel (janus/moe_w4a16.py:36-86): a tile
-// is one expert times a run of its rows; the gate_up launch fuses silu(gate) * up into its epilogue (:83), the down
-// launch scales by the routing weight (:84-85) and, unlike the reference's bf16 y buffer and reshape-sum (:140),
-// adds the fp32 product straight into an fp32 [T, H] accumulator, so the top-k combine is fp32 and rounds once.
+// accumulation. The semantics are those of the reference's per-tile kernel (janus/moe_w4a16.py:36-86): a tile is one
+// expert times a run of its rows; the gate_up launch fuses silu(gate) * up into its epilogue (:83), the down launch
+// scales by the routing weight (:84-85). Unlike the reference's bf16 y buffer and bf16 reshape-sum (:140), each
+// weighted expert output is kept in fp32 in a per-token slot and a combine pass sums a token's slots in a fixed order
+// and rounds once: the result is deterministic and carries no intermediate bf16 rounding.
 //
-// Work decomposition. A workgroup (4 waves) takes one chunk (up to 64 rows of one expert, or 64 consecutive tokens of
-// the shared expert) and one column slab. The 64 activation rows of a 128- or 256-wide k super-block are staged in LDS
-// (double-buffered) and shared by the 4 waves; each wave owns 4 MFMA column blocks of 16 weight rows, streams their
-// int4 words straight from HBM into registers (one 16-byte load per lane per 128 k), decodes them once and multiplies
-// them against all 64 rows. MFMA v_mfma_f32_16x16x32_bf16 takes the weights as its first operand, so a lane's
-// accumulator holds 4 consecutive output columns of one row. Workgroup ids are laid out so that the slabs of one chunk
-// land on the same XCD (ids are dealt to the 8 XCDs round-robin): the chunk's activation rows are then read from HBM
-// once per XCD and from its L2 afterwards.
+// Work decomposition. A workgroup (4 waves) takes one chunk (up to 96 rows of one expert, or 96 consecutive tokens of
+// the shared expert) and one column slab. Each wave owns 4 MFMA column blocks of 16 weight rows: it streams their int4
+// words from HBM into a 3-deep register ring (one 16-byte load per lane per 128 k), decodes each word once and
+// multiplies it against all of the chunk's rows. The activation rows of each 128-wide k stage go global -> LDS by
+// 16-byte direct loads into a 3-slot ring shared by the 4 waves, so loads run two stages ahead of the MFMAs without
+// holding registers. v_mfma_f32_16x16x32_bf16 takes the weights as its first operand: a lane's accumulator holds 4
+// consecutive output columns of one row. Workgroup ids are dealt to the 8 XCDs round-robin; the slabs of one chunk
+// get ids that land on the same XCD, so the chunk's activation rows come from that XCD's L2 after the first slab.
+#include <type_traits>
+
 #include "gemm.h"
 
 namespace janus {
@@ -20,9 +23,42 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kColBlocks = 4;
-constexpr int kRowBlocks = kChunkRows / 16;
+constexpr int KS = 128;                                      // k per pipeline stage: one scale group
+constexpr int kStages = 3;                                   // ring depth: loads run two stages ahead
+constexpr int kRowBytes = KS * 2;                            // one activation row of a stage (bf16)
+constexpr int kSlotBytes = kChunkRows * kRowBytes;           // one LDS ring slot
+constexpr int kLoadsPerStage = kRowBlocks + 2 * kColBlocks;  // per wave: activation rounds, weight words, scales
 
 enum { kGateUp = 0, kDown = 1 };
+
+template <int V>
+using Slot = std::integral_constant<int, V>;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Weight words and scales are loaded with inline asm, outside the compiler's load tracking (which, across the ring's
+// loop, would wait for every outstanding load before each use). The stage's registers are then tied to the explicit
+// vmcnt wait that retires their loads, so no use can be scheduled ahead of it.
+__device__ __forceinline__ u32x4 load_words_nt(const u32x4* ptr) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(ptr) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t load_u16(const uint16_t* ptr) {
+  uint32_t v;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_bind(u32x4 (&w)[4], uint32_t (&s)[4]) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3])
+               : "n"(N)
+               : "memory");
+}
 
 // One int32 word of 8 int4 weights sharing the bf16 scale `sb` -> the bf16 MFMA operand in k order 0..7.
 // t = 0x4300 | (nibble ^ 8) read as bf16 is exactly 128 + (q + 8), q the two's-complement nibble. v_dot2_f32_bf16
@@ -48,23 +84,16 @@ __device__ __forceinline__ bf16x8 decode8(uint32_t w, uint32_t sb) {
   return r;
 }
 
-template <int KS>
-struct Stage {
-  static constexpr int kWpl = KS / 32;           // weight words per lane per column block per super-block
-  static constexpr int kVecs = kWpl / 4;          // 16-byte loads of them
-  static constexpr int kLdsStride = KS + 8;       // bf16 per LDS row: consecutive rows shift by 4 banks
-  static constexpr int kAVecs = KS / 4 / 8;       // 16-byte activation loads per thread per super-block
-};
-
-template <int MODE, int KS>
+template <int MODE>
 __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p) {
-  using S = Stage<KS>;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][kChunkRows * S::kLdsStride];
+  // LDS ring of activation tiles, [stage][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16 lanes of
+  // a fragment read (same chunk, 16 rows) hit 16 different bank groups.
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * kSlotBytes];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int g = lane >> 4, nl = lane & 15;
 
-  // ---- work item: chunk c, column slab; the slabs of one chunk share an XCD ----
+  // ---- work item: chunk c, column slab ----
   const int xcd = blockIdx.x & 7, within = blockIdx.x >> 3;
   const int c = (within / p.nslab) * 8 + xcd;
   const int slab = within % p.nslab;
@@ -96,21 +125,26 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
   if (slab * kWaveCols * kWaves >= out_cols) return;
   const int col0 = slab * kWaveCols * kWaves + wave * kWaveCols;
   const bool active = col0 < out_cols;
+  const int nrb = (rows + 15) / 16;
 
-  // ---- activation row staged by this thread ----
-  const int ar = tid >> 2, apart = tid & 3;
-  const uint16_t* arow = nullptr;
-  if (ar < rows) {
+  // ---- activation rows this lane loads: round r covers rows 16r..16r+15, this wave rows 16r + 4w + (lane >> 4) ----
+  const uint16_t* asrc[kRowBlocks];
+#pragma unroll
+  for (int r = 0; r < kRowBlocks; ++r) {
+    const int row = 16 * r + 4 * wave + (lane >> 4);
+    const int rr = row < rows ? row : 0;  // padding rows re-read row 0: finite values, results discarded
+    const uint16_t* base;
     if (MODE == kGateUp) {
-      const int tok = shared ? pos0 + ar : p.sorted_ids[pos0 + ar] / p.topk;
-      arow = p.a + (long)tok * K;
+      const int tok = shared ? pos0 + rr : p.sorted_ids[pos0 + rr] / p.topk;
+      base = p.a + (long)tok * K;
     } else {
-      arow = shared ? p.a_sh + (long)(pos0 + ar) * K : p.a + (long)(pos0 + ar) * K;
+      base = shared ? p.a_sh + (long)(pos0 + rr) * K : p.a + (long)(pos0 + rr) * K;
     }
-    arow += apart * (KS / 4);
+    asrc[r] = base + (((lane & 15) ^ (row & 15)) * 8);
   }
 
-  // ---- weight rows of this lane (one per column block) ----
+  // ---- weight rows of this lane, one per column block (an idle wave reads row 0 so every wave issues the same
+  // number of loads per stage, which the vmcnt waits below count on) ----
   const u32x4* wrow[kColBlocks];
   const uint16_t* srow[kColBlocks];
 #pragma unroll
@@ -121,8 +155,8 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
     else
       n = col0 + 16 * cb + nl;
     if (!active) n = 0;
-    wrow[cb] = reinterpret_cast<const u32x4*>(wq + (long)n * (K / 8)) + g * S::kVecs;
-    srow[cb] = wsc + (long)n * (K / 128) + ((KS == 256) ? (g >> 1) : 0);
+    wrow[cb] = reinterpret_cast<const u32x4*>(wq + (long)n * (K / 8)) + g;
+    srow[cb] = wsc + (long)n * (K / 128);
   }
 
   f32x4 acc[kRowBlocks][kColBlocks];
@@ -132,82 +166,74 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
     for (int cb = 0; cb < kColBlocks; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nkb = K / KS;
-  uint4 areg[S::kAVecs];
-  u32x4 bcur[kColBlocks][S::kVecs], bnext[kColBlocks][S::kVecs];
-  uint32_t scur[kColBlocks], snext[kColBlocks];
+  u32x4 bw[kStages][kColBlocks];
+  uint32_t sc[kStages][kColBlocks];
 
-  auto load_a = [&](int kb) {
+  auto issue = [&](auto slot_c, int kb) {
+    constexpr int slot = decltype(slot_c)::value;
+    unsigned char* dst = lds + slot * kSlotBytes + 4 * wave * kRowBytes;
 #pragma unroll
-    for (int v = 0; v < S::kAVecs; ++v)
-      areg[v] = arow ? reinterpret_cast<const uint4*>(arow + kb * KS)[v] : make_uint4(0, 0, 0, 0);
-  };
-  auto store_a = [&](int buf) {
-    uint4* dst = reinterpret_cast<uint4*>(&lds[buf][ar * S::kLdsStride + apart * (KS / 4)]);
-#pragma unroll
-    for (int v = 0; v < S::kAVecs; ++v) dst[v] = areg[v];
-  };
-  auto load_b = [&](int kb, u32x4 (&bw)[kColBlocks][S::kVecs], uint32_t (&sc)[kColBlocks]) {
-    if (!active) return;
+    for (int r = 0; r < kRowBlocks; ++r)
+      __builtin_amdgcn_global_load_lds(asrc[r] + kb * KS, dst + 16 * r * kRowBytes, 16, 0, 0);
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
-#pragma unroll
-      for (int v = 0; v < S::kVecs; ++v) bw[cb][v] = __builtin_nontemporal_load(wrow[cb] + kb * (KS / 32) + v);
-      sc[cb] = srow[cb][kb * (KS / 128)];
+      bw[slot][cb] = load_words_nt(wrow[cb] + kb * (KS / 32));
+      sc[slot][cb] = load_u16(srow[cb] + kb);
     }
   };
-  auto compute = [&](int buf, const u32x4 (&bw)[kColBlocks][S::kVecs], const uint32_t (&sc)[kColBlocks]) {
-    if (!active) return;
+  auto compute = [&](auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const unsigned char* base = lds + slot * kSlotBytes;
 #pragma unroll
-    for (int t = 0; t < S::kWpl; ++t) {
+    for (int t = 0; t < KS / 32; ++t) {
       bf16x8 bfrag[kColBlocks];
 #pragma unroll
-      for (int cb = 0; cb < kColBlocks; ++cb) {
-        bfrag[cb] = decode8(bw[cb][t / 4][t % 4], sc[cb]);
-      }
+      for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = decode8(bw[slot][cb][t], sc[slot][cb]);
 #pragma unroll
       for (int rb = 0; rb < kRowBlocks; ++rb) {
-        const bf16x8 afrag =
-            *reinterpret_cast<const bf16x8*>(&lds[buf][(rb * 16 + nl) * S::kLdsStride + (g * S::kWpl + t) * 8]);
+        if (rb < nrb) {
+          const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(base + (16 * rb + nl) * kRowBytes +
+                                                                ((4 * g + t) ^ nl) * 16);
 #pragma unroll
-        for (int cb = 0; cb < kColBlocks; ++cb)
-          acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfrag[cb], afrag, acc[rb][cb], 0, 0, 0);
+          for (int cb = 0; cb < kColBlocks; ++cb)
+            acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfrag[cb], afrag, acc[rb][cb], 0, 0, 0);
+        }
       }
     }
   };
+  // Stage kb lives in ring slot kb % 3. Its loads are complete once at most one later stage's loads are outstanding;
+  // the barrier then publishes the LDS tile and retires every wave's reads of slot (kb + 2) % 3 (stage kb - 1), which
+  // the following issue overwrites.
+  auto step = [&](auto slot_c, int kb) {
+    constexpr int slot = decltype(slot_c)::value;
+    if (kb + 1 < nkb)
+      wait_vmcnt_bind<kLoadsPerStage>(bw[slot], sc[slot]);
+    else
+      wait_vmcnt_bind<0>(bw[slot], sc[slot]);
+    __builtin_amdgcn_s_barrier();
+    if (kb + 2 < nkb) issue(Slot<(slot + 2) % kStages>{}, kb + 2);
+    if (active) compute(slot_c);
+  };
 
-  load_a(0);
-  load_b(0, bcur, scur);
-  store_a(0);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; kb += 2) {
-    const bool more1 = kb + 1 < nkb;
-    if (more1) {
-      load_a(kb + 1);
-      load_b(kb + 1, bnext, snext);
-    }
-    compute(0, bcur, scur);
-    if (more1) store_a(1);
-    __syncthreads();
-    if (!more1) break;
-    const bool more2 = kb + 2 < nkb;
-    if (more2) {
-      load_a(kb + 2);
-      load_b(kb + 2, bcur, scur);
-    }
-    compute(1, bnext, snext);
-    if (more2) store_a(0);
-    __syncthreads();
+  issue(Slot<0>{}, 0);
+  if (nkb > 1) issue(Slot<1>{}, 1);
+  for (int kb = 0; kb < nkb; kb += kStages) {
+    step(Slot<0>{}, kb);
+    if (kb + 1 >= nkb) break;
+    step(Slot<1>{}, kb + 1);
+    if (kb + 2 >= nkb) break;
+    step(Slot<2>{}, kb + 2);
   }
   if (!active) return;
 
-  // ---- epilogue: lane holds rows rb*16 + nl, columns 16*cb + 4*g + i ----
+  // ---- epilogue: lane holds rows 16 rb + nl, columns 16 cb + 4 g + i ----
   if (MODE == kGateUp) {
     uint16_t* hbase = shared ? p.h_sh : p.h;
     const int hw = N / 2;
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
       const int m = rb * 16 + nl;
-      if (m >= rows) continue;
+      if (rb >= nrb || m >= rows) continue;
       uint16_t* hrow = hbase + (long)(pos0 + m) * hw;
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
@@ -227,30 +253,43 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
       const int m = rb * 16 + nl;
-      if (m >= rows) continue;
-      int tok;
+      if (rb >= nrb || m >= rows) continue;
+      int tok, slot;
       float wt;
       if (shared) {
         tok = pos0 + m;
+        slot = p.topk;
         wt = p.gamma ? p.gamma[tok] : 1.0f;
       } else {
         const int id = p.sorted_ids[pos0 + m];
         tok = id / p.topk;
+        slot = id - tok * p.topk;
         wt = p.route_w[id];
       }
-      float* orow = p.acc + (long)tok * N + col0 + 4 * g;
+      float* orow = p.slots + ((long)tok * p.nslots + slot) * N + col0 + 4 * g;
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) unsafeAtomicAdd(orow + 16 * cb + i, wt * acc[rb][cb][i]);
+        *reinterpret_cast<float4*>(orow + 16 * cb) =
+            make_float4(wt * acc[rb][cb][0], wt * acc[rb][cb][1], wt * acc[rb][cb][2], wt * acc[rb][cb][3]);
     }
   }
 }
 
-__global__ void finalize_kernel(const float4* __restrict__ acc, uint2* __restrict__ out, long n4) {
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
-    const float4 v = acc[i];
-    out[i] = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+// out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order.
+__global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4) {
+  const long n = (long)T * H4;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long t = i / H4, col = i - t * H4;
+    const float4* src = slots + t * nslots * H4 + col;
+    float4 s = src[0];
+    for (int j = 1; j < nslots; ++j) {
+      const float4 v = src[(long)j * H4];
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    out[i] = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
   }
 }
 
@@ -274,16 +313,11 @@ __global__ void dequant_kernel(const uint32_t* __restrict__ q, const uint16_t* _
 
 template <int MODE>
 int launch_gemm(const GemmParams& p, hipStream_t stream) {
-  const bool has_sh = p.n_shared_chunks > 0;
-  const int K = p.K, Ksh = has_sh ? p.K_sh : p.K;
   const int total = p.n_shared_chunks + p.max_chunks;
   if (total == 0) return JANUS_MOE_OK;
   const long grid = (long)ceil_div(total, 8) * 8 * p.nslab;
   JANUS_REQUIRE(grid < (1l << 31), JANUS_MOE_EINVAL, "grouped GEMM grid too large");
-  // 128-wide k super-blocks: 225 registers per lane, two waves per SIMD (the 256-wide variant needs 273: one wave).
-  (void)K;
-  (void)Ksh;
-  hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 128>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((w4a16_gemm_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
   JANUS_LAUNCH_CHECK(MODE == kGateUp ? "w4a16 gate_up" : "w4a16 down");
   return JANUS_MOE_OK;
 }
@@ -293,6 +327,17 @@ int launch_gemm(const GemmParams& p, hipStream_t stream) {
 int launch_gate_up(const GemmParams& p, hipStream_t stream) { return launch_gemm<kGateUp>(p, stream); }
 int launch_down(const GemmParams& p, hipStream_t stream) { return launch_gemm<kDown>(p, stream); }
 
+int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, hipStream_t stream) {
+  const long n4 = (long)T * (H / 4);
+  if (n4 == 0) return JANUS_MOE_OK;
+  long blocks = (n4 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, reinterpret_cast<const float4*>(slots),
+                     nslots, reinterpret_cast<uint2*>(out), T, H / 4);
+  JANUS_LAUNCH_CHECK("combine");
+  return JANUS_MOE_OK;
+}
+
 int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream) {
   const long words = rows * (K / 8);
   if (words == 0) return JANUS_MOE_OK;
@@ -301,17 +346,6 @@ int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16
   hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, reinterpret_cast<const uint32_t*>(q), s,
                      rows, K, reinterpret_cast<bf16x8*>(out));
   JANUS_LAUNCH_CHECK("dequant");
-  return JANUS_MOE_OK;
-}
-
-int launch_finalize(const float* acc, uint16_t* out, long n, hipStream_t stream) {
-  const long n4 = n / 4;
-  if (n4 == 0) return JANUS_MOE_OK;
-  long blocks = (n4 + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
-                     reinterpret_cast<const float4*>(acc), reinterpret_cast<uint2*>(out), n4);
-  JANUS_LAUNCH_CHECK("finalize");
   return JANUS_MOE_OK;
 }
 

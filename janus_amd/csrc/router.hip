@@ -135,16 +135,27 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const uint16_t* __re
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bf16x8 zero8 = {};
-  for (int k = k0; k < k1; k += 32) {
-    const int kk = k + 8 * g;
-    const bf16x8 a_hi = e_ok ? *reinterpret_cast<const bf16x8*>(hrow + kk) : zero8;
-    const bf16x8 a_mid = e_ok ? *reinterpret_cast<const bf16x8*>(mrow + kk) : zero8;
+  // four k-steps per iteration: their 24 fragment loads are all in flight before the first MFMA
+  constexpr int kU = 4;
+  for (int k = k0; k < k1; k += 32 * kU) {
+    bf16x8 a_hi[kU], a_mid[kU], b[kU][4];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const bf16x8 b = t_ok[tb] ? *reinterpret_cast<const bf16x8*>(xrow[tb] + kk) : zero8;
-      acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, b, acc[tb], 0, 0, 0);
-      acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_mid, b, acc[tb], 0, 0, 0);
+    for (int u = 0; u < kU; ++u) {
+      const int kk = k + 32 * u + 8 * g;
+      const bool k_ok = kk < k1;
+      a_hi[u] = (e_ok && k_ok) ? *reinterpret_cast<const bf16x8*>(hrow + kk) : zero8;
+      a_mid[u] = (e_ok && k_ok) ? *reinterpret_cast<const bf16x8*>(mrow + kk) : zero8;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+        b[u][tb] = (t_ok[tb] && k_ok) ? *reinterpret_cast<const bf16x8*>(xrow[tb] + kk) : zero8;
     }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi[u], b[u][tb], acc[tb], 0, 0, 0);
+        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_mid[u], b[u][tb], acc[tb], 0, 0, 0);
+      }
   }
   // lane holds experts blockIdx.y*64 + 16*wave + 4g + i of token t0 + 16tb + nl
   const int ebase = blockIdx.y * 64 + wave * 16 + 4 * g;
@@ -325,7 +336,9 @@ __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
     const int e = lane + 64 * j;
     if (j < nj && e < E) {
       float s = 0.f;
-      for (int z = 0; z < nslice; ++z) s += partial[((long)z * T + t) * Epad + e];
+#pragma unroll
+      for (int z = 0; z < kMaxHv; ++z)
+        if (z < nslice) s += partial[((long)z * T + t) * Epad + e];
       if (bias) s += bias[e];
       av[j] = s;
     }
