@@ -7,12 +7,13 @@
 //
 // Work decomposition. A workgroup (4 waves) takes one chunk (up to 96 rows of one expert, or 96 consecutive tokens of
 // the shared expert) and one column slab. Each wave owns 4 MFMA column blocks of 16 weight rows: it streams their int4
-// words from HBM into a 3-deep register ring (one 16-byte load per lane per 128 k), decodes each word once and
-// multiplies it against all of the chunk's rows. The activation rows of each 128-wide k stage go global -> LDS by
-// 16-byte direct loads into a 3-slot ring shared by the 4 waves, so loads run two stages ahead of the MFMAs without
-// holding registers. v_mfma_f32_16x16x32_bf16 takes the weights as its first operand: a lane's accumulator holds 4
-// consecutive output columns of one row. Workgroup ids are dealt to the 8 XCDs round-robin; the slabs of one chunk
-// get ids that land on the same XCD, so the chunk's activation rows come from that XCD's L2 after the first slab.
+// words from HBM into a 2-deep register ring (one 16-byte load per lane per 128 k), decodes each word once and
+// multiplies it against all of the chunk's rows. The activation rows of each 128-wide k stage are staged through
+// registers into an LDS double buffer shared by the 4 waves, one stage ahead of the MFMAs (they are mostly L2 hits:
+// every slab of a chunk reads the same rows). v_mfma_f32_16x16x32_bf16 takes the weights as its first operand: a
+// lane's accumulator holds 4 consecutive output columns of one row. Workgroup ids are dealt to the 8 XCDs round-robin;
+// the slabs of one chunk get ids that land on the same XCD, so the chunk's activation rows come from that XCD's L2
+// after the first slab.
 #include <type_traits>
 
 #include "gemm.h"
@@ -24,71 +25,119 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kColBlocks = 4;
 constexpr int KS = 128;                                      // k per pipeline stage: one scale group
-constexpr int kStages = 3;                                   // ring depth: loads run two stages ahead
+constexpr int kStages = 2;                                   // weight ring depth: loads run one stage ahead
 constexpr int kRowBytes = KS * 2;                            // one activation row of a stage (bf16)
-constexpr int kSlotBytes = kChunkRows * kRowBytes;           // one LDS ring slot
-constexpr int kLoadsPerStage = kRowBlocks + 2 * kColBlocks;  // per wave: activation rounds, weight words, scales
+constexpr int kSlotBytes = kChunkRows * kRowBytes;           // one LDS activation buffer
 
 enum { kGateUp = 0, kDown = 1 };
 
 template <int V>
 using Slot = std::integral_constant<int, V>;
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+// Compile-time loop: f(integral_constant<int, I>) for I in [0, N).
+template <int... Is, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, F&& f) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, static_cast<F&&>(f));
 }
 
-// Weight words and scales are loaded with inline asm, outside the compiler's load tracking (which, across the ring's
-// loop, would wait for every outstanding load before each use). The stage's registers are then tied to the explicit
-// vmcnt wait that retires their loads, so no use can be scheduled ahead of it.
-__device__ __forceinline__ u32x4 load_words_nt(const u32x4* ptr) {
-  u32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(ptr) : "memory");
-  return v;
+// Barrier without the memory fence __syncthreads() adds (which would wait for every outstanding load, prefetches
+// included): LDS writes are completed first, and the asm keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The k pipeline. Activations: global -> registers (one stage ahead) -> LDS double buffer, written once the stage
+// before has been consumed. Weight words and scales: a kStages-slot register ring, loads kStages - 1 stages ahead. Every load is an
+// ordinary compiler-tracked load; with NKB fixed the loop is unrolled, so the compiler's waits are exact counts.
+//   load_a(kb) / store_a(buf)          stage kb's activation rows into registers / registers into LDS buffer buf
+//   load_b(slot, kb)                   stage kb's weight words and scales into ring slot `slot`
+//   compute(slot, buf)                 MFMAs of the stage held in ring slot `slot` and LDS buffer buf
+template <int NKB, typename LoadA, typename StoreA, typename LoadB, typename Compute>
+__device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool active, LoadA&& load_a,
+                                                                   StoreA&& store_a, LoadB&& load_b,
+                                                                   Compute&& compute) {
+  auto step = [&](auto slot_c, int kb) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    constexpr int ahead = kStages - 1;  // weight loads run this many stages ahead
+    if (kb + ahead < nkb) load_b(Slot<(slot + ahead) % kStages>{}, kb + ahead);
+    if (active) compute(slot_c, kb & 1);
+    if (kb + 1 < nkb) {
+      store_a((kb + 1) & 1);
+      if (kb + 2 < nkb) load_a(kb + 2);
+    }
+    lds_barrier();
+  };
+  load_a(0);
+  static_for<kStages - 1>([&](auto s_c) __attribute__((always_inline)) {
+    if (decltype(s_c)::value < nkb) load_b(s_c, decltype(s_c)::value);
+  });
+  store_a(0);
+  if (nkb > 1) load_a(1);
+  lds_barrier();
+  if constexpr (NKB > 0) {
+    static_for<NKB>([&](auto kb_c) __attribute__((always_inline)) {
+      step(Slot<decltype(kb_c)::value % kStages>{}, decltype(kb_c)::value);
+    });
+  } else {
+    for (int kb = 0; kb < nkb; kb += kStages) {
+      static_for<kStages>([&](auto s_c) __attribute__((always_inline)) {
+        if (kb + decltype(s_c)::value < nkb) step(s_c, kb + decltype(s_c)::value);
+      });
+    }
+  }
 }
-__device__ __forceinline__ uint32_t load_u16(const uint16_t* ptr) {
-  uint32_t v;
-  asm volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
-  return v;
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_bind(u32x4 (&w)[4], uint32_t (&s)[4]) {
-  asm volatile("s_waitcnt vmcnt(%8)"
-               : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3])
-               : "n"(N)
-               : "memory");
+
+// d = a.lo * b.lo + a.hi * b.hi + c (bf16 pairs, fp32 c and d) in the 3-operand VOP3P form. Left to itself the compiler
+// picks the accumulating VOP2 form, which needs a copy of c into d before every use.
+__device__ __forceinline__ float dot2_bf16(bf16x2 a, bf16x2 b, float c) {
+  float d;
+  asm("v_dot2_f32_bf16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
 }
 
 // One int32 word of 8 int4 weights sharing the bf16 scale `sb` -> the bf16 MFMA operand in k order 0..7.
 // t = 0x4300 | (nibble ^ 8) read as bf16 is exactly 128 + (q + 8), q the two's-complement nibble. v_dot2_f32_bf16
 // with the scale in one half of the other operand and 0 in the other half gives (q + 136) * s - 136 * s, every step
 // exact in fp32, i.e. q * s exactly; the conversion to bf16 rounds it once to nearest even: bf16(q * s).
-__device__ __forceinline__ bf16x8 decode8(uint32_t w, uint32_t sb) {
-  const bf16x2 s_lo = __builtin_bit_cast(bf16x2, sb);
-  const bf16x2 s_hi = __builtin_bit_cast(bf16x2, sb << 16);
-  const float c = -136.0f * __uint_as_float(sb << 16);
+// Per word: 3 shifts, 4 and-xor (one v_bitop3 each), 8 dot2, 4 packed conversions.
+struct Scale {
+  bf16x2 lo, hi;  // (s, 0) and (0, s)
+  float c;        // -136 s
+};
+__device__ __forceinline__ Scale make_scale(uint32_t sb) {
+  Scale r;
+  r.lo = __builtin_bit_cast(bf16x2, sb);
+  r.hi = __builtin_bit_cast(bf16x2, sb << 16);
+  r.c = -136.0f * __uint_as_float(sb << 16);
+  return r;
+}
+__device__ __forceinline__ bf16x8 decode8(uint32_t w, const Scale& s) {
   const bf16x2 t0 = __builtin_bit_cast(bf16x2, (w & 0x000F000Fu) ^ 0x43084308u);
   const bf16x2 t1 = __builtin_bit_cast(bf16x2, ((w >> 4) & 0x000F000Fu) ^ 0x43084308u);
   const bf16x2 t2 = __builtin_bit_cast(bf16x2, ((w >> 8) & 0x000F000Fu) ^ 0x43084308u);
   const bf16x2 t3 = __builtin_bit_cast(bf16x2, ((w >> 12) & 0x000F000Fu) ^ 0x43084308u);
   bf16x8 r;
-  r[0] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t0, s_lo, c, false));
-  r[1] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t1, s_lo, c, false));
-  r[2] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t2, s_lo, c, false));
-  r[3] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t3, s_lo, c, false));
-  r[4] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t0, s_hi, c, false));
-  r[5] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t1, s_hi, c, false));
-  r[6] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t2, s_hi, c, false));
-  r[7] = static_cast<__bf16>(__builtin_amdgcn_fdot2_f32_bf16(t3, s_hi, c, false));
+  r[0] = static_cast<__bf16>(dot2_bf16(t0, s.lo, s.c));
+  r[1] = static_cast<__bf16>(dot2_bf16(t1, s.lo, s.c));
+  r[2] = static_cast<__bf16>(dot2_bf16(t2, s.lo, s.c));
+  r[3] = static_cast<__bf16>(dot2_bf16(t3, s.lo, s.c));
+  r[4] = static_cast<__bf16>(dot2_bf16(t0, s.hi, s.c));
+  r[5] = static_cast<__bf16>(dot2_bf16(t1, s.hi, s.c));
+  r[6] = static_cast<__bf16>(dot2_bf16(t2, s.hi, s.c));
+  r[7] = static_cast<__bf16>(dot2_bf16(t3, s.hi, s.c));
   return r;
 }
+__device__ __forceinline__ bf16x8 decode8(uint32_t w, uint32_t sb) { return decode8(w, make_scale(sb)); }
 
-template <int MODE>
-__global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p) {
-  // LDS ring of activation tiles, [stage][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16 lanes of
-  // a fragment read (same chunk, 16 rows) hit 16 different bank groups.
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * kSlotBytes];
+// NKB: k stages (K / 128) fixed at compile time, the whole k loop unrolled so the compiler's wait counts for the
+// weight registers are exact (a runtime loop makes it wait for every outstanding load); 0 = runtime K.
+template <int MODE, int NKB>
+__global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
+  // LDS double buffer of activation tiles, [buffer][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16
+  // lanes of a fragment read (same chunk, 16 rows) hit 16 different bank groups.
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int g = lane >> 4, nl = lane & 15;
@@ -127,26 +176,32 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
   const bool active = col0 < out_cols;
   const int nrb = (rows + 15) / 16;
 
-  // ---- activation rows this lane loads: round r covers rows 16r..16r+15, this wave rows 16r + 4w + (lane >> 4) ----
-  const uint16_t* asrc[kRowBlocks];
+  // ---- activation rows this lane stages: round r covers rows 16r..16r+15, this wave rows 16r + 4w + (lane >> 4), 16
+  // lanes per row each taking one 16-byte chunk (chunk lane & 15) ----
+  // 32-bit byte offsets from wave-uniform bases (SGPR base + VGPR offset addressing) keep the pointer state small.
+  const unsigned char* abase;
+  if (MODE == kGateUp)
+    abase = reinterpret_cast<const unsigned char*>(p.a);
+  else
+    abase = reinterpret_cast<const unsigned char*>(shared ? p.a_sh : p.a);
+  uint32_t aoff[kRowBlocks];
 #pragma unroll
   for (int r = 0; r < kRowBlocks; ++r) {
     const int row = 16 * r + 4 * wave + (lane >> 4);
     const int rr = row < rows ? row : 0;  // padding rows re-read row 0: finite values, results discarded
-    const uint16_t* base;
-    if (MODE == kGateUp) {
-      const int tok = shared ? pos0 + rr : p.sorted_ids[pos0 + rr] / p.topk;
-      base = p.a + (long)tok * K;
-    } else {
-      base = shared ? p.a_sh + (long)(pos0 + rr) * K : p.a + (long)(pos0 + rr) * K;
-    }
-    asrc[r] = base + (((lane & 15) ^ (row & 15)) * 8);
+    int arow;
+    if (MODE == kGateUp)
+      arow = shared ? pos0 + rr : p.sorted_ids[pos0 + rr] / p.topk;
+    else
+      arow = pos0 + rr;
+    aoff[r] = (uint32_t)arow * (uint32_t)(K * 2) + (lane & 15) * 16;
   }
+  const int arow0 = 4 * wave + (lane >> 4);  // this lane's row in round 0
 
-  // ---- weight rows of this lane, one per column block (an idle wave reads row 0 so every wave issues the same
-  // number of loads per stage, which the vmcnt waits below count on) ----
-  const u32x4* wrow[kColBlocks];
-  const uint16_t* srow[kColBlocks];
+  // ---- weight rows of this lane, one per column block (an idle wave reads row 0 and discards it) ----
+  const unsigned char* wbase = reinterpret_cast<const unsigned char*>(wq);
+  const unsigned char* sbase = reinterpret_cast<const unsigned char*>(wsc);
+  uint32_t woff[kColBlocks], soff[kColBlocks];
 #pragma unroll
   for (int cb = 0; cb < kColBlocks; ++cb) {
     int n;
@@ -155,8 +210,8 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
     else
       n = col0 + 16 * cb + nl;
     if (!active) n = 0;
-    wrow[cb] = reinterpret_cast<const u32x4*>(wq + (long)n * (K / 8)) + g;
-    srow[cb] = wsc + (long)n * (K / 128);
+    woff[cb] = (uint32_t)n * (uint32_t)(K / 2) + g * 16;
+    soff[cb] = (uint32_t)n * (uint32_t)(K / 64);
   }
 
   f32x4 acc[kRowBlocks][kColBlocks];
@@ -165,30 +220,42 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nkb = K / KS;
+  const int nkb = NKB > 0 ? NKB : K / KS;
   u32x4 bw[kStages][kColBlocks];
   uint32_t sc[kStages][kColBlocks];
 
-  auto issue = [&](auto slot_c, int kb) {
-    constexpr int slot = decltype(slot_c)::value;
-    unsigned char* dst = lds + slot * kSlotBytes + 4 * wave * kRowBytes;
+  u32x4 areg[kRowBlocks];  // native vectors: an array of HIP's uint4 struct is not promoted to registers
+  auto load_a = [&](int kb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r)
-      __builtin_amdgcn_global_load_lds(asrc[r] + kb * KS, dst + 16 * r * kRowBytes, 16, 0, 0);
+    for (int r = 0; r < kRowBlocks; ++r) areg[r] = *reinterpret_cast<const u32x4*>(abase + aoff[r] + kb * (KS * 2));
+  };
+  auto store_a = [&](int buf) __attribute__((always_inline)) {
+    unsigned char* dst = lds + buf * kSlotBytes;
 #pragma unroll
-    for (int cb = 0; cb < kColBlocks; ++cb) {
-      bw[slot][cb] = load_words_nt(wrow[cb] + kb * (KS / 32));
-      sc[slot][cb] = load_u16(srow[cb] + kb);
+    for (int r = 0; r < kRowBlocks; ++r) {
+      const int row = 16 * r + arow0;
+      *reinterpret_cast<u32x4*>(dst + row * kRowBytes + (((lane & 15) ^ (row & 15)) * 16)) = areg[r];
     }
   };
-  auto compute = [&](auto slot_c) {
+  auto load_b = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    const unsigned char* base = lds + slot * kSlotBytes;
+#pragma unroll
+    for (int cb = 0; cb < kColBlocks; ++cb) {
+      bw[slot][cb] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2)));
+      sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * 2);
+    }
+  };
+  auto compute = [&](auto slot_c, int buf) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const unsigned char* base = lds + buf * kSlotBytes;
+    Scale scl[kColBlocks];
+#pragma unroll
+    for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = make_scale(sc[slot][cb]);
 #pragma unroll
     for (int t = 0; t < KS / 32; ++t) {
       bf16x8 bfrag[kColBlocks];
 #pragma unroll
-      for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = decode8(bw[slot][cb][t], sc[slot][cb]);
+      for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = decode8(bw[slot][cb][t], scl[cb]);
 #pragma unroll
       for (int rb = 0; rb < kRowBlocks; ++rb) {
         if (rb < nrb) {
@@ -201,29 +268,7 @@ __global__ void __launch_bounds__(kThreads) w4a16_gemm_kernel(const GemmParams p
       }
     }
   };
-  // Stage kb lives in ring slot kb % 3. Its loads are complete once at most one later stage's loads are outstanding;
-  // the barrier then publishes the LDS tile and retires every wave's reads of slot (kb + 2) % 3 (stage kb - 1), which
-  // the following issue overwrites.
-  auto step = [&](auto slot_c, int kb) {
-    constexpr int slot = decltype(slot_c)::value;
-    if (kb + 1 < nkb)
-      wait_vmcnt_bind<kLoadsPerStage>(bw[slot], sc[slot]);
-    else
-      wait_vmcnt_bind<0>(bw[slot], sc[slot]);
-    __builtin_amdgcn_s_barrier();
-    if (kb + 2 < nkb) issue(Slot<(slot + 2) % kStages>{}, kb + 2);
-    if (active) compute(slot_c);
-  };
-
-  issue(Slot<0>{}, 0);
-  if (nkb > 1) issue(Slot<1>{}, 1);
-  for (int kb = 0; kb < nkb; kb += kStages) {
-    step(Slot<0>{}, kb);
-    if (kb + 1 >= nkb) break;
-    step(Slot<1>{}, kb + 1);
-    if (kb + 2 >= nkb) break;
-    step(Slot<2>{}, kb + 2);
-  }
+  run_pipeline<NKB>(nkb, active, load_a, store_a, load_b, compute);
   if (!active) return;
 
   // ---- epilogue: lane holds rows 16 rb + nl, columns 16 cb + 4 g + i ----
@@ -317,7 +362,16 @@ int launch_gemm(const GemmParams& p, hipStream_t stream) {
   if (total == 0) return JANUS_MOE_OK;
   const long grid = (long)ceil_div(total, 8) * 8 * p.nslab;
   JANUS_REQUIRE(grid < (1l << 31), JANUS_MOE_EINVAL, "grouped GEMM grid too large");
-  hipLaunchKernelGGL((w4a16_gemm_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
+  const bool same_k = p.n_shared_chunks == 0 || p.K_sh == p.K;
+  const int nkb = same_k ? p.K / KS : 0;
+  const dim3 g((unsigned)grid), b(kThreads);
+  switch (nkb) {
+    case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2>), g, b, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 4>), g, b, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 8>), g, b, 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 16>), g, b, 0, stream, p); break;
+    default: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 0>), g, b, 0, stream, p); break;
+  }
   JANUS_LAUNCH_CHECK(MODE == kGateUp ? "w4a16 gate_up" : "w4a16 down");
   return JANUS_MOE_OK;
 }
