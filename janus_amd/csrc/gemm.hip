@@ -320,19 +320,30 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
   }
 }
 
-// out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order.
+// out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order. The loads of up to 8 slots
+// are issued together before the additions.
 __global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4) {
+  constexpr int kBatch = 8;
   const long n = (long)T * H4;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
     const long t = i / H4, col = i - t * H4;
     const float4* src = slots + t * nslots * H4 + col;
     float4 s = src[0];
-    for (int j = 1; j < nslots; ++j) {
-      const float4 v = src[(long)j * H4];
-      s.x += v.x;
-      s.y += v.y;
-      s.z += v.z;
-      s.w += v.w;
+    for (int j0 = 1; j0 < nslots; j0 += kBatch) {
+      f32x4 v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (j0 + j < nslots)
+          v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + (long)(j0 + j) * H4));
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (j0 + j < nslots) {
+          s.x += v[j][0];
+          s.y += v[j][1];
+          s.z += v[j][2];
+          s.w += v[j][3];
+        }
+      }
     }
     out[i] = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
   }

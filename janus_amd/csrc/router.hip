@@ -7,7 +7,7 @@
 //   router_logits  approximate logits for every (token, expert): bf16 MFMA over a two-plane split of the fp32 weight
 //                  (w = hi + mid + r, |r| <= 2^-16 |w|), fp32 accumulation, split over k in 512-wide slices.
 //   router_select  one wave per token: the candidate set {e : approx_e >= approx_(k) - 2 delta_t} provably contains the
-//                  top_k, where delta_t >= |approx - exact| (Cauchy-Schwarz on the split residual plus a 2^-12 relative
+//                  top_k, where delta_t >= |approx - exact| (Cauchy-Schwarz on the split residual plus a 2^-15 relative
 //                  allowance for fp32 accumulation). Only candidates in a cluster of approximate values closer than
 //                  2 delta that reaches into the top_k need their exact logit: an fp64 dot product whose error bound
 //                  decides the fp32 rounding, or, within that bound of a rounding midpoint, a double-double sum.
@@ -113,49 +113,72 @@ __global__ void __launch_bounds__(256) router_meta_kernel(int E, RouterPrep p) {
 }
 
 // ---- approximate logits ---------------------------------------------------------------------------------------
-// grid (ceil(T/64), ceil(E/64), ceil(H/512)); wave w: experts blockIdx.y*64 + 16w .. +15, tokens blockIdx.x*64 .. +63.
-__global__ void __launch_bounds__(256) router_logits_kernel(const uint16_t* __restrict__ x, RouterPrep p, int T, int H,
+// grid (ceil(T/64), Epad/64, ceil(H/512)); wave w: experts blockIdx.y*64 + 16w .. +15, tokens blockIdx.x*64 .. +63 of
+// the k slice blockIdx.z. The slice of the 64 x rows sits in LDS (shared by the 4 waves); each wave streams its 16
+// expert rows of both planes from global memory, kAhead k-steps ahead.
+//
+// Rounding. Every bf16 x bf16 product is exact in fp32. Each k-step of 32 forms a fresh block sum of 64 products
+// (hi plane, then mid plane, chained in two MFMAs from zero) that VALU adds to the running fp32 sum, so any product
+// passes through at most 32 + 33 roundings in its block, 16 block additions and up to 8 slice additions (in
+// router_select): 89 roundings of at most 2^-23 relative each (truncating arithmetic assumed), well inside the 2^-15
+// allowance the selection uses.
+constexpr int kSteps = kSlice / 32;  // k-steps per slice
+constexpr int kAhead = 8;            // weight fragment loads in flight per wave
+constexpr int kTileT = 64;           // tokens per workgroup
+constexpr int kXRowBytes = kSlice * 2;
+
+__global__ void __launch_bounds__(256, 2) router_logits_kernel(const uint16_t* __restrict__ x, RouterPrep p, int T, int H,
                                                             int E, int Epad, float* __restrict__ partial) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, nl = lane & 15;
-  const int e = blockIdx.y * 64 + wave * 16 + nl;
-  const int t0 = blockIdx.x * 64;
-  const int k0 = blockIdx.z * kSlice, k1 = min(H, k0 + kSlice);
-  const bool e_ok = e < E;
-  const uint16_t* hrow = p.hi + (long)(e_ok ? e : 0) * H;
-  const uint16_t* mrow = p.mid + (long)(e_ok ? e : 0) * H;
-  const uint16_t* xrow[4];
-  bool t_ok[4];
+  __shared__ __attribute__((aligned(16))) unsigned char xs[kTileT * kXRowBytes];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, nl = lane & 15;
+  const int t0 = blockIdx.x * kTileT;
+  const int k0 = blockIdx.z * kSlice, klen = min(H - k0, kSlice);
+
+  // x tile: 64 rows x 64 16-byte chunks, chunk c of row r stored at chunk position c ^ (r & 15). Buffer loads write it
+  // straight into LDS (lane l of a load fills position l of the row); a chunk past the slice or a row past T is given
+  // an offset beyond the buffer, which the hardware returns as zeros.
+  const __amdgpu_buffer_rsrc_t xrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)((long)T * H * 2), 0x00020000);
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int t = t0 + tb * 16 + nl;
-    t_ok[tb] = t < T;
-    xrow[tb] = x + (long)(t_ok[tb] ? t : 0) * H;
+  for (int i = 0; i < kTileT / 4; ++i) {
+    const int row = wave * (kTileT / 4) + i, t = t0 + row, c = lane ^ (row & 15);
+    const uint32_t off = (t < T && c * 8 < klen) ? (uint32_t)(((long)t * H + k0 + c * 8) * 2) : 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (__attribute__((address_space(3))) void*)(xs + row * kXRowBytes),
+                                             16, off, 0, 0, 0);
   }
+  const int e = blockIdx.y * 64 + wave * 16 + nl;
+  const bool e_ok = e < E;
+  const uint16_t* hrow = p.hi + (long)(e_ok ? e : 0) * H + k0 + 8 * g;
+  const uint16_t* mrow = p.mid + (long)(e_ok ? e : 0) * H + k0 + 8 * g;
+  u32x4 wh[kAhead], wm[kAhead];
+  auto load_w = [&](int slot, int step) __attribute__((always_inline)) {
+    const bool ok = e_ok && 32 * step < klen;
+    wh[slot] = ok ? *reinterpret_cast<const u32x4*>(hrow + 32 * step) : u32x4{0, 0, 0, 0};
+    wm[slot] = ok ? *reinterpret_cast<const u32x4*>(mrow + 32 * step) : u32x4{0, 0, 0, 0};
+  };
+#pragma unroll
+  for (int s = 0; s < kAhead; ++s) load_w(s, s);
+  __syncthreads();
+
   f32x4 acc[4];
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16x8 zero8 = {};
-  // four k-steps per iteration: their 24 fragment loads are all in flight before the first MFMA
-  constexpr int kU = 4;
-  for (int k = k0; k < k1; k += 32 * kU) {
-    bf16x8 a_hi[kU], a_mid[kU], b[kU][4];
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int kk = k + 32 * u + 8 * g;
-      const bool k_ok = kk < k1;
-      a_hi[u] = (e_ok && k_ok) ? *reinterpret_cast<const bf16x8*>(hrow + kk) : zero8;
-      a_mid[u] = (e_ok && k_ok) ? *reinterpret_cast<const bf16x8*>(mrow + kk) : zero8;
+  for (int s = 0; s < kSteps; ++s) {
+    const int slot = s % kAhead;
+    const bf16x8 hf = __builtin_bit_cast(bf16x8, wh[slot]);
+    const bf16x8 mf = __builtin_bit_cast(bf16x8, wm[slot]);
+    if (s + kAhead < kSteps) load_w(slot, s + kAhead);
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
-        b[u][tb] = (t_ok[tb] && k_ok) ? *reinterpret_cast<const bf16x8*>(xrow[tb] + kk) : zero8;
+    for (int tb = 0; tb < 4; ++tb) {
+      const int row = 16 * tb + nl;
+      const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xs + row * kXRowBytes + (((4 * s + g) ^ nl) * 16));
+      f32x4 b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hf, xf, zero4, 0, 0, 0);
+      b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, xf, b, 0, 0, 0);
+      acc[tb] += b;
+      asm volatile("" : "+v"(acc[tb]));  // add now: left alone, the compiler keeps every step's block sum live
     }
-#pragma unroll
-    for (int u = 0; u < kU; ++u)
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi[u], b[u][tb], acc[tb], 0, 0, 0);
-        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_mid[u], b[u][tb], acc[tb], 0, 0, 0);
-      }
   }
   // lane holds experts blockIdx.y*64 + 16*wave + 4g + i of token t0 + 16tb + nl
   const int ebase = blockIdx.y * 64 + wave * 16 + 4 * g;
@@ -195,18 +218,31 @@ __device__ float round_dd_to_f32(double hi, double lo) {
   return ((lo > 0.0) == (hi > rd)) ? n : r;
 }
 
-// Wave-cooperative exact logit of (x of this lane, expert row wrow). xv: the lane's x vectors (8 bf16 each at
-// h = 512 j + 8 lane). Returns the correctly rounded fp32 dot product in every lane.
-__device__ float exact_logit(const uint4 (&xv)[kMaxHv], int nhv, int H, const float* __restrict__ wrow, double bound) {
+// Wave-cooperative exact logits of this lane's x (8 bf16 at h = 512 j + 8 lane) against the rows ids[0..n) of w
+// (wave-uniform, n <= kExactBatch). The loads of all n rows are in flight together. out[c]: the correctly rounded fp32
+// dot product, in every lane. bound[c] >= ||x|| ||w_c||.
+constexpr int kExactBatch = 4;  // array size; rows per batch: exact_batch(NHV)
+constexpr int exact_batch(int nhv) { return nhv <= 2 ? 4 : nhv == 4 ? 2 : 1; }
+
+template <int NHV>
+struct XRow {
+  uint4 v[NHV];
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+template <int NHV>
+__device__ __forceinline__ float xval(const XRow<NHV>& x, int j, int i) {
+  const uint32_t wd = i < 2 ? x.v[j].x : i < 4 ? x.v[j].y : i < 6 ? x.v[j].z : x.v[j].w;
+  return (i & 1) ? bf16_hi(wd) : bf16_lo(wd);
+}
+template <int NHV>
+__device__ __forceinline__ void load_wrow(const float* __restrict__ wrow, int H, bool ok, float (&wv)[NHV][8]) {
   const int lane = threadIdx.x & 63;
-  double acc = 0.0;
-  int nterms = 0;
-  float wv[kMaxHv][8];
 #pragma unroll
-  for (int j = 0; j < kMaxHv; ++j) {
-    if (j >= nhv) break;
+  for (int j = 0; j < NHV; ++j) {
     const int h0 = 512 * j + 8 * lane;
-    if (h0 < H) {
+    if (ok && h0 < H) {
       const float4 a = *reinterpret_cast<const float4*>(wrow + h0);
       const float4 b = *reinterpret_cast<const float4*>(wrow + h0 + 4);
       wv[j][0] = a.x; wv[j][1] = a.y; wv[j][2] = a.z; wv[j][3] = a.w;
@@ -216,52 +252,80 @@ __device__ float exact_logit(const uint4 (&xv)[kMaxHv], int nhv, int H, const fl
       for (int i = 0; i < 8; ++i) wv[j][i] = 0.f;
     }
   }
-#pragma unroll
-  for (int j = 0; j < kMaxHv; ++j) {
-    if (j >= nhv) break;
-    const uint32_t words[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float xf = __uint_as_float(i & 1 ? (words[i / 2] & 0xFFFF0000u) : (words[i / 2] << 16));
-      acc = fma((double)xf, (double)wv[j][i], acc);
-    }
-    nterms += 8;
-  }
-  const double v = wave_sum_f64(acc);
-  // |v - exact| <= (terms per lane + tree depth) * 2^-53 * sum|x w| <= that * ||x|| ||w||
-  const double err = (double)(nterms + 6) * 0x1p-53 * bound;
-  const float r = (float)v;
-  const double rd = (double)r;
-  const double dn = 0.5 * (rd + (double)f32_next_down(r));
-  const double up = 0.5 * (rd + (double)f32_next_up(r));
-  if (v - dn > err && up - v > err) return r;
-  // Within the bound of a rounding midpoint: double-double accumulation.
+}
+
+// The exact logit when an fp64 sum lies within its error bound of an fp32 rounding midpoint: double-double
+// accumulation of the same products. Rare; kept out of line so the common path keeps its registers.
+template <int NHV>
+__device__ __noinline__ float exact_logit_dd(XRow<NHV> x, const float* __restrict__ wrow, int H) {
+  float wv[NHV][8];
+  load_wrow<NHV>(wrow, H, true, wv);
   double hi = 0.0, lo = 0.0;
 #pragma unroll
-  for (int j = 0; j < kMaxHv; ++j) {
-    if (j >= nhv) break;
-    const uint32_t words[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+  for (int j = 0; j < NHV; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float xf = __uint_as_float(i & 1 ? (words[i / 2] & 0xFFFF0000u) : (words[i / 2] << 16));
-      double s, e;
-      two_sum(hi, (double)xf * (double)wv[j][i], s, e);
-      hi = s;
-      lo += e;
+      double s2, e2;
+      two_sum(hi, (double)xval(x, j, i) * (double)wv[j][i], s2, e2);
+      hi = s2;
+      lo += e2;
     }
-  }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const double h2 = __shfl_down(hi, off), l2 = __shfl_down(lo, off);
-    double s, e;
-    two_sum(hi, h2, s, e);
-    lo = lo + l2 + e;
-    hi = s;
+    double s2, e2;
+    two_sum(hi, h2, s2, e2);
+    lo = lo + l2 + e2;
+    hi = s2;
   }
-  double s, e;
-  two_sum(hi, lo, s, e);
-  const float out = round_dd_to_f32(s, e);
-  return __shfl(out, 0);
+  double s2, e2;
+  two_sum(hi, lo, s2, e2);
+  return __shfl(round_dd_to_f32(s2, e2), 0);
+}
+
+template <int NHV>
+__device__ void exact_logits(const XRow<NHV>& x, int H, const float* __restrict__ w, const int (&ids)[kExactBatch],
+                             int n, const double (&bound)[kExactBatch], float (&out)[kExactBatch]) {
+  float wv[kExactBatch][NHV][8];
+#pragma unroll
+  for (int c = 0; c < kExactBatch; ++c)
+    if (c < exact_batch(NHV)) load_wrow<NHV>(w + (long)ids[c] * H, H, c < n, wv[c]);
+  double v[kExactBatch];
+#pragma unroll
+  for (int c = 0; c < exact_batch(NHV); ++c) {
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < NHV; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fma((double)xval(x, j, i), (double)wv[c][j][i], acc);
+    v[c] = acc;
+    __builtin_amdgcn_sched_barrier(0);  // one row's fp64 operands live at a time
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+    for (int c = 0; c < exact_batch(NHV); ++c) v[c] += __shfl_xor(v[c], off);
+#pragma unroll
+  for (int c = 0; c < exact_batch(NHV); ++c) v[c] = __shfl(v[c], 0);  // one value per wave: the branches below are uniform
+#pragma unroll
+  for (int c = 0; c < exact_batch(NHV); ++c) {
+    if (c >= n) break;
+    // |v - exact| <= (terms per lane + tree depth) * 2^-53 * sum|x w| <= that * ||x|| ||w||
+    const double err = (double)(8 * NHV + 6) * 0x1p-53 * bound[c];
+    const float r = (float)v[c];
+    const double rd = (double)r;
+    const double dn = 0.5 * (rd + (double)f32_next_down(r));
+    const double up = 0.5 * (rd + (double)f32_next_up(r));
+    out[c] = (v[c] - dn > err && up - v[c] > err) ? r : exact_logit_dd<NHV>(x, w + (long)ids[c] * H, H);
+  }
+}
+
+// exact_logits in a function of its own, for rare paths whose caller should not reserve its registers.
+template <int NHV>
+__device__ __noinline__ void exact_logits_outlined(XRow<NHV> x, int H, const float* __restrict__ w,
+                                                   const int (&ids)[kExactBatch], int n,
+                                                   const double (&bound)[kExactBatch], float (&out)[kExactBatch]) {
+  exact_logits<NHV>(x, H, w, ids, n, bound, out);
 }
 
 // ---- selection -----------------------------------------------------------------------------------------------
@@ -283,6 +347,28 @@ __device__ void rank_sort(const Cand* cand, Cand* out, int n) {
   }
 }
 
+// Order-preserving map of fp32 onto uint32 (larger float <-> larger key), and back.
+__device__ __forceinline__ uint32_t f32_key(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_f32(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Rank of (v, e) among the nc candidates held by lanes 0..nc-1 (value descending, id ascending), read lane by lane.
+__device__ __forceinline__ int lane_rank(float v, int e, int nc) {
+  int r = 0;
+  for (int j = 0; j < nc; ++j) {
+    const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+    const int ej = __builtin_amdgcn_readlane(e, j);
+    r += better(vj, ej, v, e);
+  }
+  return r;
+}
+
+// One wave per token. NJ: experts per lane (expert lane + 64 j), NHV: 16-byte x vectors per lane.
+template <int NHV, int NJ>
 __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ w, RouterPrep p, const float* __restrict__ bias,
     const uint16_t* __restrict__ wsg, int T, int H, int E, int Epad, int nslice, int top_k,
@@ -295,28 +381,41 @@ __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;  // a whole wave; no workgroup barriers below
 
-  // x row in registers, norm, shared gate
-  const int nhv = (H + 511) / 512;
-  uint4 xv[kMaxHv];
+  // every load up front: x row, shared-gate row, approximate logit slices, bias
+  XRow<NHV> xrow;
+  uint4 (&xv)[NHV] = xrow.v;
+  uint4 gv[NHV];
+#pragma unroll
+  for (int j = 0; j < NHV; ++j) {
+    const int h0 = 512 * j + 8 * lane;
+    const bool ok = h0 < H;
+    xv[j] = ok ? *reinterpret_cast<const uint4*>(x + (long)t * H + h0) : make_uint4(0, 0, 0, 0);
+    gv[j] = (ok && wsg) ? *reinterpret_cast<const uint4*>(wsg + h0) : make_uint4(0, 0, 0, 0);
+  }
+  float av[NJ];
+  const float* prow = partial + (long)t * Epad + lane;
+  const long zstride = (long)T * Epad;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const bool ok = lane + 64 * j < E;
+    float sj = 0.f;
+#pragma unroll
+    for (int z = 0; z < kMaxHv; ++z)
+      if (z < nslice) sj += ok ? prow[z * zstride + 64 * j] : 0.f;
+    if (bias) sj += ok ? bias[lane + 64 * j] : 0.f;
+    av[j] = ok ? sj : -__builtin_inff();
+  }
+
+  // norm of x and the shared-expert gate
   float ss = 0.f, gdot = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxHv; ++j) {
-    xv[j] = make_uint4(0, 0, 0, 0);
-    if (j < nhv) {
-      const int h0 = 512 * j + 8 * lane;
-      if (h0 < H) {
-        xv[j] = *reinterpret_cast<const uint4*>(x + (long)t * H + h0);
-        const uint32_t words[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-        uint4 gw = wsg ? *reinterpret_cast<const uint4*>(wsg + h0) : make_uint4(0, 0, 0, 0);
-        const uint32_t gws[4] = {gw.x, gw.y, gw.z, gw.w};
+  for (int j = 0; j < NHV; ++j) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float xf = __uint_as_float(i & 1 ? (words[i / 2] & 0xFFFF0000u) : (words[i / 2] << 16));
-          const float gf = __uint_as_float(i & 1 ? (gws[i / 2] & 0xFFFF0000u) : (gws[i / 2] << 16));
-          ss = fmaf(xf, xf, ss);
-          gdot = fmaf(xf, gf, gdot);
-        }
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float xf = xval(xrow, j, i);
+      const uint32_t gw = i < 2 ? gv[j].x : i < 4 ? gv[j].y : i < 6 ? gv[j].z : gv[j].w;
+      ss = fmaf(xf, xf, ss);
+      gdot = fmaf(xf, (i & 1) ? bf16_hi(gw) : bf16_lo(gw), gdot);
     }
   }
   ss = wave_sum_f32(ss);
@@ -325,91 +424,134 @@ __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
     if (lane == 0 && gamma) gamma[t] = 1.0f / (1.0f + __expf(-gdot));
   }
   const double xnorm = sqrt((double)ss) * (1.0 + 1e-5);
-  const double delta = xnorm * (p.meta[0] + 0x1p-12 * p.meta[1]) + 1e-30;
+  const double delta = xnorm * (p.meta[0] + 0x1p-15 * p.meta[1]) + 1e-30;
 
-  // approximate logits: lane holds experts lane + 64 j
-  const int nj = (E + 63) / 64;
-  float av[kMaxJ];
+  // k-th largest approximate value: binary search on the order-preserving keys, counting with ballots
+  uint32_t key[NJ];
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
-    av[j] = -__builtin_inff();
-    const int e = lane + 64 * j;
-    if (j < nj && e < E) {
-      float s = 0.f;
+  for (int j = 0; j < NJ; ++j) key[j] = lane + 64 * j < E ? f32_key(av[j]) : 0u;
+  uint32_t tau = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t trial = tau | (1u << bit);
+    int cnt = 0;
 #pragma unroll
-      for (int z = 0; z < kMaxHv; ++z)
-        if (z < nslice) s += partial[((long)z * T + t) * Epad + e];
-      if (bias) s += bias[e];
-      av[j] = s;
-    }
+    for (int j = 0; j < NJ; ++j) cnt += __popcll(ballot(key[j] >= trial));
+    if (cnt >= top_k) tau = trial;
   }
-  // k-th largest approximate value (ties to the lower id)
-  uint32_t taken = 0;
-  float vk = 0.f;
-  for (int r = 0; r < top_k; ++r) {
-    float bv = -__builtin_inff();
-    int be = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) {
-      const int e = lane + 64 * j;
-      if (j < nj && e < E && !((taken >> j) & 1) && better(av[j], e, bv, be)) {
-        bv = av[j];
-        be = e;
-      }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oe = __shfl_xor(be, off);
-      if (better(ov, oe, bv, be)) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    if ((be & 63) == lane) taken |= 1u << (be >> 6);
-    vk = bv;
-  }
+  const float vk = key_f32(tau);
   // bias rounding and the split / accumulation allowance
   const float d2 = (float)(2.0 * delta) + (bias ? 4.0f * __builtin_fabsf(vk) * 0x1p-24f : 0.f);
   const float theta = vk - d2;
-  // candidates in LDS
+  // candidates, compacted in id order into LDS
   int nc = 0;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
-    const int e = lane + 64 * j;
-    const bool pred = j < nj && e < E && av[j] >= theta;
+  for (int j = 0; j < NJ; ++j) {
+    const bool pred = lane + 64 * j < E && av[j] >= theta;
     const uint64_t m = ballot(pred);
-    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    if (pred) cand[nc + __popcll(m & below)] = Cand{av[j], e};
+    if (pred) cand[nc + __popcll(m & below)] = Cand{av[j], lane + 64 * j};
     nc += __popcll(m);
   }
   wave_sync();
-  rank_sort(cand, sorted, nc);
-  wave_sync();
-  // which candidates need their exact logit: members of a cluster (adjacent gaps < d2) that reaches into the top_k.
-  // Flags for all candidates first (in cand[].e, free after the sort), from approximate values only.
-  if (lane == 0) {
-    int s = 0;
-    for (int i = 0; i < nc; ++i) {
-      if (i > 0 && sorted[i - 1].v - sorted[i].v >= d2) s = i;  // s: start of i's cluster
-      int e2 = i;
-      while (e2 + 1 < nc && sorted[e2].v - sorted[e2 + 1].v < d2) ++e2;
-      cand[i].e = (e2 > s || (i > s)) && (s < top_k);
+
+  if (nc <= 64) {
+    // lane i holds candidate i; ranks by reading the other lanes
+    float vi = -__builtin_inff();
+    int ei = 0x7fffffff;
+    if (lane < nc) {
+      vi = cand[lane].v;
+      ei = cand[lane].e;
     }
-  }
-  wave_sync();
-  for (int i = 0; i < nc; ++i) {
-    if (cand[i].e) {  // wave-uniform
-      const int e = sorted[i].e;
-      float l = exact_logit(xv, nhv, H, w + (long)e * H, xnorm * p.wnorm[e] * (1.0 + 1e-6));
-      if (bias) l = l + bias[e];
-      if (lane == 0) sorted[i].v = l;
+    int r = lane_rank(vi, ei, nc);
+    if (lane < nc) sorted[r] = Cand{vi, ei};
+    wave_sync();
+    if (lane < nc) {
+      vi = sorted[lane].v;
+      ei = sorted[lane].e;
     }
+    // members of a cluster (adjacent gaps < d2) that reaches into the top_k need their exact logit
+    const bool in = lane < nc;
+    const float vp = __shfl_up(vi, 1);
+    const uint64_t starts = ballot(in && (lane == 0 || vp - vi >= d2));
+    const uint64_t upto = (2ull << lane) - 1;            // bits 0..lane
+    const int cs = 63 - __clzll(starts & upto);            // this lane's cluster start (bit 0 is always set)
+    const uint64_t next = starts & ~upto;
+    const int last = next ? __builtin_ctzll(next) - 1 : nc - 1;  // this lane's cluster end
+    uint64_t f = ballot(in && last > cs && cs < top_k);
+    while (f) {
+      int ids[kExactBatch], pos[kExactBatch];
+      double bnd[kExactBatch];
+      int n = 0;
+#pragma unroll
+      for (int c = 0; c < kExactBatch; ++c) {
+        pos[c] = 0;
+        ids[c] = 0;
+        bnd[c] = 0.0;
+        if (c < exact_batch(NHV) && f) {
+          pos[c] = __builtin_ctzll(f);
+          f &= f - 1;
+          ids[c] = __builtin_amdgcn_readlane(ei, pos[c]);
+          bnd[c] = xnorm * p.wnorm[ids[c]] * (1.0 + 1e-6);
+          n = c + 1;
+        }
+      }
+      float l[kExactBatch];
+      exact_logits<NHV>(xrow, H, w, ids, n, bnd, l);
+#pragma unroll
+      for (int c = 0; c < kExactBatch; ++c)
+        if (c < n && lane == pos[c]) vi = bias ? l[c] + bias[ids[c]] : l[c];
+    }
+    r = lane_rank(vi, ei, nc);
+    wave_sync();
+    if (lane < nc && r < top_k) cand[r] = Cand{vi, ei};
+    wave_sync();
+  } else {
+    // many near-equal values: the same steps through LDS
+    rank_sort(cand, sorted, nc);
+    wave_sync();
+    if (lane == 0) {
+      int cs = 0;
+      for (int i = 0; i < nc; ++i) {
+        if (i > 0 && sorted[i - 1].v - sorted[i].v >= d2) cs = i;  // cs: start of i's cluster
+        int e2 = i;
+        while (e2 + 1 < nc && sorted[e2].v - sorted[e2 + 1].v < d2) ++e2;
+        cand[i].e = e2 > cs && cs < top_k;
+      }
+    }
+    wave_sync();
+    for (int base = 0; base < nc; base += 64) {
+      uint64_t f = ballot(base + lane < nc && cand[base + lane].e);
+      while (f) {
+        int ids[kExactBatch], pos[kExactBatch];
+        double bnd[kExactBatch];
+        int n = 0;
+#pragma unroll
+        for (int c = 0; c < kExactBatch; ++c) {
+          pos[c] = 0;
+          ids[c] = 0;
+          bnd[c] = 0.0;
+          if (c < exact_batch(NHV) && f) {
+            pos[c] = base + __builtin_ctzll(f);
+            f &= f - 1;
+            ids[c] = sorted[pos[c]].e;
+            bnd[c] = xnorm * p.wnorm[ids[c]] * (1.0 + 1e-6);
+            n = c + 1;
+          }
+        }
+        float l[kExactBatch];
+        exact_logits_outlined<NHV>(xrow, H, w, ids, n, bnd, l);
+        if (lane == 0) {
+#pragma unroll
+          for (int c = 0; c < kExactBatch; ++c)
+            if (c < n) sorted[pos[c]].v = bias ? l[c] + bias[ids[c]] : l[c];
+        }
+      }
+    }
+    wave_sync();
+    rank_sort(sorted, cand, nc);
+    wave_sync();
   }
-  wave_sync();
-  rank_sort(sorted, cand, nc);
-  wave_sync();
-  // renormalised softmax over the top_k
+  // renormalised softmax over the top_k (cand[0..top_k) in slot order)
   float v = -__builtin_inff();
   int e = 0;
   if (lane < top_k) {
@@ -459,17 +601,38 @@ int launch_route(const uint16_t* x, const float* w, const void* prep, const floa
                      E, Epad, ws.partial);
   JANUS_LAUNCH_CHECK("router_logits");
   const size_t smem = (size_t)4 * 2 * E * sizeof(Cand);
-  hipLaunchKernelGGL(router_select_kernel, dim3(ceil_div(T, 4)), dim3(kSelThreads), smem, stream, x, w, p, bias, wsg, T,
-                     H, E, Epad, nslice, top_k, ws.partial, topk_idx, topk_w, gamma);
+  const dim3 sg(ceil_div(T, 4)), sb(kSelThreads);
+  const int nhv = ceil_div(H, 512), nj = ceil_div(E, 64);
+#define JANUS_SELECT(NHV_, NJ_)                                                                                   \
+  hipLaunchKernelGGL((router_select_kernel<NHV_, NJ_>), sg, sb, smem, stream, x, w, p, bias, wsg, T, H, E, Epad, \
+                     nslice, top_k, ws.partial, topk_idx, topk_w, gamma)
+#define JANUS_SELECT_NJ(NHV_)       \
+  if (nj <= 2)                      \
+    JANUS_SELECT(NHV_, 2);          \
+  else if (nj <= 4)                 \
+    JANUS_SELECT(NHV_, 4);          \
+  else                              \
+    JANUS_SELECT(NHV_, 16);
+  if (nhv <= 1) {
+    JANUS_SELECT_NJ(1)
+  } else if (nhv <= 2) {
+    JANUS_SELECT_NJ(2)
+  } else if (nhv <= 4) {
+    JANUS_SELECT_NJ(4)
+  } else {
+    JANUS_SELECT_NJ(8)
+  }
+#undef JANUS_SELECT_NJ
+#undef JANUS_SELECT
   JANUS_LAUNCH_CHECK("router_select");
   return JANUS_MOE_OK;
 }
 
 int check_route_sizes(int T, int H, int E, int top_k) {
   JANUS_REQUIRE(T >= 0 && H > 0 && H % 32 == 0 && H <= 512 * kMaxHv && E > 0 && E <= 64 * kMaxJ && E % 4 == 0 &&
-                    top_k > 0 && top_k <= 64 && top_k <= E,
+                    top_k > 0 && top_k <= 64 && top_k <= E && (long)T * H * 2 < (1l << 31),
                 JANUS_MOE_EINVAL, "router: unsupported sizes T=%d H=%d E=%d top_k=%d (need H %% 32 == 0, H <= %d, "
-                "E %% 4 == 0, E <= %d, top_k <= min(64, E))", T, H, E, top_k, 512 * kMaxHv, 64 * kMaxJ);
+                "E %% 4 == 0, E <= %d, top_k <= min(64, E), T * H < 2^30)", T, H, E, top_k, 512 * kMaxHv, 64 * kMaxJ);
   return JANUS_MOE_OK;
 }
 
