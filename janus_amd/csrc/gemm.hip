@@ -89,12 +89,11 @@ __device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool
   }
 }
 
-// d = a.lo * b.lo + a.hi * b.hi + c (bf16 pairs, fp32 c and d) in the 3-operand VOP3P form. Left to itself the compiler
-// picks the accumulating VOP2 form, which needs a copy of c into d before every use.
+// d = a.lo * b.lo + a.hi * b.hi + c (bf16 pairs, fp32 c and d). The library is built without the accumulating VOP2
+// form of this instruction (target feature dot13-insts off): that form overwrites c, so every use of the shared c
+// below would need a copy first.
 __device__ __forceinline__ float dot2_bf16(bf16x2 a, bf16x2 b, float c) {
-  float d;
-  asm("v_dot2_f32_bf16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
+  return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
 }
 
 // One int32 word of 8 int4 weights sharing the bf16 scale `sb` -> the bf16 MFMA operand in k order 0..7.
