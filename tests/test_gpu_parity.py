@@ -160,6 +160,27 @@ def test_fused_moe_tiny(gpu):
 
 # ---- whole block -----------------------------------------------------------------------------------------------
 
+def test_tiny_block_against_golden_fixture(gpu):
+    """tests/golden/tiny_layer.npz: routing and align plan bit-exact, the block output within the layer bar."""
+    from pathlib import Path
+
+    g = np.load(Path(__file__).resolve().parent / "golden" / "tiny_layer.npz")
+    cfg = synth.CONFIGS["tiny"]
+    L = synth.layer(cfg)
+    x = synth.activations(cfg).to(gpu)
+    blk = W4A16SparseMoeBlock.from_tensors(L, cfg.k).to(gpu)
+    with torch.no_grad():
+        out = blk(x)
+        _, w, idx = blk.gate(x)
+    assert np.array_equal(idx.cpu().numpy(), g["topk_idx"])
+    np.testing.assert_allclose(w.cpu().numpy(), g["topk_w"], rtol=1e-4, atol=1e-6)
+    sorted_ids, expert_ids, total = align(idx, cfg.E, 16)
+    assert np.array_equal(sorted_ids.cpu().numpy(), g["sorted_ids"])
+    assert np.array_equal(expert_ids.cpu().numpy(), g["expert_ids"])
+    assert np.array_equal(total.cpu().numpy(), g["total"])
+    assert_layer_close(bf16_np(out), O.bf16_from_bits(g["out_bits"]), "tiny golden")
+
+
 def _block(cfg, gpu, seed=17):
     L = synth.layer(cfg, seed)
     blk = W4A16SparseMoeBlock.from_tensors(L, cfg.k).to(gpu)
