@@ -2,14 +2,17 @@
 I=512, shared expert 512, int4 group-128 weights), one step = one full layer forward (router, routed experts,
 gated shared expert, combine) through the HIP path.
 
-    python bench.py [--steps K] [--warmup W] [--config headline] [--no-cpu] [--eager]
+    python bench.py [--steps K] [--warmup W] [--config headline] [--no-cpu] [--no-pmc] [--gpus 1]
 
-Timing: W untimed forwards, then K forwards replayed from one HIP graph capture of the layer (the way the reference
-serves, a level per graph), bracketed by device synchronisation. Inputs and weights are resident in HBM before the
-timed region. Separately, an eager pass with stage events (the library's profiling hook) times each kernel stage;
-the dominant kernel's average duration gives the roofline entry. The CPU baseline is the reference's CPU algorithm
-(dequantise-per-call + padded bmm, oracle/cpu_bmm.py) on the same inputs, on all host cores, on a bounded sample.
-Prints one JSON line.
+Timed region: W untimed forwards, then K forwards launched back to back on one stream, bracketed by device
+synchronisation. Inputs and weights are resident in HBM before it starts. In every timed step the library records
+HIP events on its launch stream at the stage boundaries (janus_moe_profile_events), each step into its own events,
+so the per-kernel averages cover exactly the timed steps. The dominant kernel (the gate_up GEMM) gives the roofline
+entry; its HBM traffic per launch comes from two rocprofv3 --pmc child runs of this script (FETCH_SIZE, then
+WRITE_SIZE), each scaled by what the same counter reads for a device copy of known size. The same layer replayed
+from a HIP graph is timed afterwards and reported as graph_tokens_per_s. The CPU baseline is the reference's CPU
+algorithm (dequantise-per-call + padded bmm, oracle/cpu_bmm.py) on the same inputs, on all host cores, on a bounded
+sample. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -18,8 +21,12 @@ import ctypes
 import json
 import os
 import platform
+import sqlite3
+import subprocess
 import sys
+import tempfile
 import time
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -27,6 +34,10 @@ import torch
 METRIC = "MoE layer tokens/s at T=2048 (35B-A3B shape); % of HBM/MFMA roofline"
 HBM_PEAK = 8.0e12        # bytes/s, MI355X
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 FLOP/s, MI355X
+STAGES = ("route", "align", "gate_up", "down", "combine")
+GATE_UP_KERNEL = "w4a16_gemm_kernel<0,"
+COPY_MIB = 256
+HERE = Path(__file__).resolve().parent
 
 
 def layer_work(cfg, idx: np.ndarray) -> dict:
@@ -67,6 +78,76 @@ def cpu_baseline(layer, x, k, budget_s: float = 30.0) -> dict:
                       f"({t:.2f} s per call, torch CPU, {platform.processor() or platform.machine()})"}
 
 
+def make_layer(name: str, dev: torch.device):
+    from janus_amd import synth
+    from janus_amd.block import W4A16SparseMoeBlock
+
+    cfg = synth.CONFIGS[name]
+    layer = synth.layer(cfg)
+    x = synth.activations(cfg).to(dev)
+    blk = W4A16SparseMoeBlock.from_tensors(layer, cfg.k).to(dev)
+    return cfg, layer, x, blk
+
+
+# ---- counters (child runs under rocprofv3) ---------------------------------------------------------------------
+
+def _pmc_child(args) -> int:
+    """What the profiled child runs: a few eager layer forwards, or one device copy of COPY_MIB MiB."""
+    dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return 0
+    _, _, x, blk = make_layer(args.config, dev)
+    with torch.no_grad():
+        for _ in range(4):
+            blk(x)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _counter_per_dispatch(db: Path, counter: str, kernel_substr: str) -> float:
+    """Mean over dispatches of `counter` (summed over its hardware instances) for kernels whose name contains
+    kernel_substr."""
+    con = sqlite3.connect(db)
+    per = {}
+    for name, disp, cn, v in con.execute("select name, dispatch_id, counter_name, counter_value from pmc_events"):
+        if cn == counter and kernel_substr in name.replace(" ", ""):
+            per[disp] = per.get(disp, 0.0) + v
+    if not per:
+        raise RuntimeError(f"no {counter} samples for {kernel_substr} in {db}")
+    return float(np.mean(list(per.values())))
+
+
+def _profile(counter: str, child_args: list[str], kernel_substr: str, timeout: int = 150) -> float:
+    with tempfile.TemporaryDirectory() as tmp:
+        cmd = ["rocprofv3", "--pmc", counter, "-d", tmp, "-o", "run", "--", sys.executable, str(HERE / "bench.py"),
+               "--pmc-child", *child_args]
+        subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=timeout, check=True)
+        dbs = sorted(Path(tmp).rglob("*results.db"))
+        if not dbs:
+            raise RuntimeError("rocprofv3 wrote no results database")
+        return _counter_per_dispatch(dbs[0], counter, kernel_substr)
+
+
+def pmc_traffic(config: str) -> dict:
+    """HBM bytes per gate_up launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by the ratio of
+    the known bytes of a COPY_MIB MiB device copy to what the same counter reads for it."""
+    copy_bytes = COPY_MIB << 20
+    fetch_copy = _profile("FETCH_SIZE", ["--copy-calibration", str(COPY_MIB)], "copy")
+    write_copy = _profile("WRITE_SIZE", ["--copy-calibration", str(COPY_MIB)], "copy")
+    f_fetch, f_write = copy_bytes / (fetch_copy * 1024), copy_bytes / (write_copy * 1024)
+    fetch = _profile("FETCH_SIZE", ["--config", config], GATE_UP_KERNEL) * 1024 * f_fetch
+    write = _profile("WRITE_SIZE", ["--config", config], GATE_UP_KERNEL) * 1024 * f_write
+    return {"fetch_bytes": fetch, "write_bytes": write, "fetch_scale": f_fetch, "write_scale": f_write}
+
+
+# ---- the measurement --------------------------------------------------------------------------------------------
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,39 +155,28 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replay")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run a plain device copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--no-pmc", action="store_true", help="skip the rocprofv3 traffic passes (traffic: null)")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--copy-calibration", type=int, default=0, help=argparse.SUPPRESS)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this MoE layer runs on a single MI355X by design (asked for "
               f"--gpus {args.gpus}, WORLD_SIZE {world}); run it with --gpus 1", file=sys.stderr)
         return 2
+    if args.pmc_child:
+        return _pmc_child(args)
+
+    from janus_amd import _lib
 
     dev = torch.device("cuda", 0)
-    if args.copy_calibration:
-        n = args.copy_calibration << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}))
-        return 0
-
-    from janus_amd import _lib, synth
-    from janus_amd.block import W4A16SparseMoeBlock
-
-    cfg = synth.CONFIGS[args.config]
-    layer = synth.layer(cfg)
-    x = synth.activations(cfg).to(dev)
-    blk = W4A16SparseMoeBlock.from_tensors(layer, cfg.k).to(dev)
+    cfg, layer, x, blk = make_layer(args.config, dev)
     with torch.no_grad():
-        out = blk(x)                            # router prep, first launch
+        blk(x)                                  # router prep, first launch
         _, _, idx = blk.gate(x)
     torch.cuda.synchronize()
     work = layer_work(cfg, idx.cpu().numpy())
+    L = _lib.lib()
 
     def step():
         with torch.no_grad():
@@ -115,59 +185,65 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    graph = None
-    if not args.eager:
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            step()
-        torch.cuda.current_stream(dev).wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            out = step()
-        for _ in range(3):
-            graph.replay()
+
+    # timed region: K eager forwards, each recording its own stage events on the launch stream
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(args.steps)]
+    for row in events:
+        for e in row:
+            e.record()                          # creates the underlying hipEvent
+    handles = [(ctypes.c_void_p * len(row))(*[ctypes.c_void_p(e.cuda_event) for e in row]) for row in events]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        if graph is not None:
-            graph.replay()
-        else:
-            step()
+    for i in range(args.steps):
+        L.janus_moe_profile_events(handles[i], len(STAGES) + 1)
+        step()
+    L.janus_moe_profile_events(None, 0)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed / args.steps * 1e3
+    stage_ms = np.array([[row[j].elapsed_time(row[j + 1]) for j in range(len(STAGES))] for row in events])
+    stage_us = {n: float(v) * 1e3 for n, v in zip(STAGES, stage_ms.mean(0))}
 
-    # stage timing with events on the launch stream (eager)
-    L = _lib.lib()
-    names = ("route", "align", "gate_up", "down", "finalize")
-    sums = np.zeros(len(names))
-    reps = max(5, min(args.steps, 50))
-    for _ in range(reps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
-        for e in ev:
-            e.record()                          # creates the underlying hipEvent
-        handles = (ctypes.c_void_p * 6)(*[ctypes.c_void_p(e.cuda_event) for e in ev])
-        L.janus_moe_profile_events(handles, 6)
+    # the same forward replayed from a HIP graph (the reference serves under graphs)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
         step()
-        L.janus_moe_profile_events(None, 0)
-        torch.cuda.synchronize()
-        sums += [ev[i].elapsed_time(ev[i + 1]) for i in range(5)]
-    stage_us = {n: float(v / reps * 1e3) for n, v in zip(names, sums)}
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_s = (time.perf_counter() - t1) / args.steps
 
     gu_s = stage_us["gate_up"] * 1e-6
     t_step = ms * 1e-3
     t_roof = max(work["flops"] / MFMA_BF16_PEAK, work["bytes"] / HBM_PEAK)
-    gu_bound_hbm = work["gu_bytes"] / HBM_PEAK >= work["gu_flops"] / MFMA_BF16_PEAK
-    if gu_bound_hbm:
+    if work["gu_bytes"] / HBM_PEAK >= work["gu_flops"] / MFMA_BF16_PEAK:
         ach = work["gu_bytes"] / gu_s / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": ach / (HBM_PEAK / 1e9)}
     else:
         ach = work["gu_flops"] / gu_s / 1e12
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                 "frac": ach / (MFMA_BF16_PEAK / 1e12)}
-    roof.update({"kernel": "w4a16_gemm_kernel<gate_up>", "algorithmic_bytes": work["gu_bytes"],
-                 "algorithmic_flops": work["gu_flops"], "avg_us": stage_us["gate_up"], "traffic": None})
+    traffic, traffic_note = None, "skipped (--no-pmc)"
+    if not args.no_pmc:
+        try:
+            t = pmc_traffic(args.config)
+            traffic = t["fetch_bytes"] + t["write_bytes"]
+            traffic_note = (f"rocprofv3 FETCH_SIZE x {t['fetch_scale']:.3f} + WRITE_SIZE x {t['write_scale']:.3f} "
+                            f"(scales from a {COPY_MIB} MiB copy): fetch {t['fetch_bytes']:.4g} B, "
+                            f"write {t['write_bytes']:.4g} B per launch")
+        except Exception as exc:  # no profiler on this machine: the entry stays null, with the reason
+            traffic_note = f"unavailable: {type(exc).__name__}: {exc}"[:300]
+    roof.update({"traffic": traffic, "kernel": "w4a16_gemm_kernel<gate_up>", "algorithmic_bytes": work["gu_bytes"],
+                 "algorithmic_flops": work["gu_flops"], "avg_us": stage_us["gate_up"], "traffic_source": traffic_note})
 
     result = {
         "metric": METRIC, "value": cfg.T / t_step, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -176,12 +252,13 @@ def main() -> int:
         "config": {"workload": f"W4A16 MoE layer {cfg.name}: T={cfg.T} H={cfg.H} E={cfg.E} top{cfg.k} I={cfg.I} "
                                f"shared I={cfg.I_s}", "T": cfg.T, "H": cfg.H, "experts": cfg.E, "top_k": cfg.k,
                    "I": cfg.I, "I_shared": cfg.I_s, "codec": "int4 group-128, bf16 scales",
-                   "timing": "eager launches" if graph is None else "HIP graph replay"},
+                   "timing": "eager launches on one stream, stage events per step"},
         "roofline": roof,
         "layer_roofline": {"t_roof_us": t_roof * 1e6, "t_us": t_step * 1e6, "frac": t_roof / t_step,
                            "bound": "hbm" if work["bytes"] / HBM_PEAK >= work["flops"] / MFMA_BF16_PEAK else "mfma",
                            "flops": work["flops"], "bytes": work["bytes"], "n_hit": work["n_hit"]},
         "stages_us": stage_us,
+        "graph_tokens_per_s": cfg.T / graph_s, "graph_ms_per_step": graph_s * 1e3,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layer, x, cfg.k)

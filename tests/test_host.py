@@ -199,3 +199,17 @@ def test_cpu_block_matches_oracle():
     assert (tidx.numpy() == idx).mean() > 0.99
     got = O.bf16_values(out)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
+
+
+def test_cpu_baseline_port_matches_oracle():
+    """oracle/cpu_bmm.py, the reference's CPU algorithm that bench.py times, computes the same layer (bf16-rounded
+    like the reference) on the tiny config."""
+    from oracle import cpu_bmm
+
+    cfg = synth.CONFIGS["tiny"]
+    Lw = synth.layer(cfg)
+    x = synth.activations(cfg)
+    out = cpu_bmm.layer_forward(Lw, x, cfg.k)
+    ref, _, _, _ = O.block_forward(O.numpy_layer(Lw), O.bf16_values(x), cfg.k)
+    got = O.bf16_values(out)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
