@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import re
 import json
 import os
 import platform
@@ -35,7 +36,7 @@ METRIC = "MoE layer tokens/s at T=2048 (35B-A3B shape); % of HBM/MFMA roofline"
 HBM_PEAK = 8.0e12        # bytes/s, MI355X
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 FLOP/s, MI355X
 STAGES = ("route", "align", "gate_up", "down", "combine")
-GATE_UP_KERNEL = "w4a16_gemm_kernel<0,"
+GATE_UP_KERNEL = r"w4a16_\w+_kernel<0,"     # the gate_up instantiations (pipelined or generic)
 COPY_MIB = 256
 HERE = Path(__file__).resolve().parent
 
@@ -111,12 +112,12 @@ def _pmc_child(args) -> int:
 
 
 def _counter_per_dispatch(db: Path, counter: str, kernel_substr: str) -> float:
-    """Mean over dispatches of `counter` (summed over its hardware instances) for kernels whose name contains
-    kernel_substr."""
+    """Mean over dispatches of `counter` (summed over its hardware instances) for kernels whose name matches the regular
+    expression kernel_substr."""
     con = sqlite3.connect(db)
     per = {}
     for name, disp, cn, v in con.execute("select name, dispatch_id, counter_name, counter_value from pmc_events"):
-        if cn == counter and kernel_substr in name.replace(" ", ""):
+        if cn == counter and re.search(kernel_substr, name.replace(" ", "")):
             per[disp] = per.get(disp, 0.0) + v
     if not per:
         raise RuntimeError(f"no {counter} samples for {kernel_substr} in {db}")
@@ -138,8 +139,8 @@ def pmc_traffic(config: str) -> dict:
     """HBM bytes per gate_up launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by the ratio of
     the known bytes of a COPY_MIB MiB device copy to what the same counter reads for it."""
     copy_bytes = COPY_MIB << 20
-    fetch_copy = _profile("FETCH_SIZE", ["--copy-calibration", str(COPY_MIB)], "copy")
-    write_copy = _profile("WRITE_SIZE", ["--copy-calibration", str(COPY_MIB)], "copy")
+    fetch_copy = _profile("FETCH_SIZE", ["--copy-calibration", str(COPY_MIB)], "copyBuffer")
+    write_copy = _profile("WRITE_SIZE", ["--copy-calibration", str(COPY_MIB)], "copyBuffer")
     f_fetch, f_write = copy_bytes / (fetch_copy * 1024), copy_bytes / (write_copy * 1024)
     fetch = _profile("FETCH_SIZE", ["--config", config], GATE_UP_KERNEL) * 1024 * f_fetch
     write = _profile("WRITE_SIZE", ["--config", config], GATE_UP_KERNEL) * 1024 * f_write

@@ -89,43 +89,32 @@ __device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool
   }
 }
 
-// d = a.lo * b.lo + a.hi * b.hi + c (bf16 pairs, fp32 c and d). The library is built without the accumulating VOP2
-// form of this instruction (target feature dot13-insts off): that form overwrites c, so every use of the shared c
-// below would need a copy first.
-__device__ __forceinline__ float dot2_bf16(bf16x2 a, bf16x2 b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
-}
-
 // One int32 word of 8 int4 weights sharing the bf16 scale `sb` -> the bf16 MFMA operand in k order 0..7.
-// t = 0x4300 | (nibble ^ 8) read as bf16 is exactly 128 + (q + 8), q the two's-complement nibble. v_dot2_f32_bf16
-// with the scale in one half of the other operand and 0 in the other half gives (q + 136) * s - 136 * s, every step
-// exact in fp32, i.e. q * s exactly; the conversion to bf16 rounds it once to nearest even: bf16(q * s).
-// Per word: 3 shifts, 4 and-xor (one v_bitop3 each), 8 dot2, 4 packed conversions.
+// Each nibble, its top bit flipped (offset binary n = q + 8, 0..15), goes into the low four bits of a byte. Read as an
+// fp8 e4m3 byte (OCP: bias 7, subnormals) such a byte is exactly n * 2^-9: exponent field 0 gives the subnormals
+// 0..7 * 2^-9, exponent field 1 the normals (8 + m) * 2^-9. v_cvt_pk_f32_fp8 widens two of them per instruction, and
+// fma(n 2^-9, 512 s, -8 s) = q s exactly: the product has at most 12 significant bits and the sum is the exact
+// q s, which has at most 12 too, so the fma's rounding changes nothing. The packed conversion to bf16 then rounds once
+// to nearest even: bf16(q * s). Per word: two masks (one with a shift), four widenings, eight fmas, four packs.
 struct Scale {
-  bf16x2 lo, hi;  // (s, 0) and (0, s)
-  float c;        // -136 s
+  float m, c;  // 512 s and -8 s
 };
 __device__ __forceinline__ Scale make_scale(uint32_t sb) {
-  Scale r;
-  r.lo = __builtin_bit_cast(bf16x2, sb);
-  r.hi = __builtin_bit_cast(bf16x2, sb << 16);
-  r.c = -136.0f * __uint_as_float(sb << 16);
-  return r;
+  const float s = __uint_as_float(sb << 16);
+  return Scale{512.0f * s, -8.0f * s};
 }
 __device__ __forceinline__ bf16x8 decode8(uint32_t w, const Scale& s) {
-  const bf16x2 t0 = __builtin_bit_cast(bf16x2, (w & 0x000F000Fu) ^ 0x43084308u);
-  const bf16x2 t1 = __builtin_bit_cast(bf16x2, ((w >> 4) & 0x000F000Fu) ^ 0x43084308u);
-  const bf16x2 t2 = __builtin_bit_cast(bf16x2, ((w >> 8) & 0x000F000Fu) ^ 0x43084308u);
-  const bf16x2 t3 = __builtin_bit_cast(bf16x2, ((w >> 12) & 0x000F000Fu) ^ 0x43084308u);
+  // bytes j of lo / hi: elements 2j / 2j + 1, as n = nibble ^ 8 (v_bitop3 truth table 0x6A: (S0 & S1) ^ S2)
+  const uint32_t lo = __builtin_amdgcn_bitop3_b32(w, 0x0F0F0F0Fu, 0x08080808u, 0x6A);
+  const uint32_t hi = __builtin_amdgcn_bitop3_b32(w >> 4, 0x0F0F0F0Fu, 0x08080808u, 0x6A);
+  const float2_t l0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);  // elements 0, 2
+  const float2_t l1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);   // elements 4, 6
+  const float2_t h0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false);  // elements 1, 3
+  const float2_t h1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);   // elements 5, 7
+  const float v[8] = {l0[0], h0[0], l0[1], h0[1], l1[0], h1[0], l1[1], h1[1]};
   bf16x8 r;
-  r[0] = static_cast<__bf16>(dot2_bf16(t0, s.lo, s.c));
-  r[1] = static_cast<__bf16>(dot2_bf16(t1, s.lo, s.c));
-  r[2] = static_cast<__bf16>(dot2_bf16(t2, s.lo, s.c));
-  r[3] = static_cast<__bf16>(dot2_bf16(t3, s.lo, s.c));
-  r[4] = static_cast<__bf16>(dot2_bf16(t0, s.hi, s.c));
-  r[5] = static_cast<__bf16>(dot2_bf16(t1, s.hi, s.c));
-  r[6] = static_cast<__bf16>(dot2_bf16(t2, s.hi, s.c));
-  r[7] = static_cast<__bf16>(dot2_bf16(t3, s.hi, s.c));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = static_cast<__bf16>(fmaf(v[j], s.m, s.c));
   return r;
 }
 __device__ __forceinline__ bf16x8 decode8(uint32_t w, uint32_t sb) { return decode8(w, make_scale(sb)); }
@@ -240,7 +229,7 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
-      bw[slot][cb] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2)));
+      bw[slot][cb] = *reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2));
       sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * 2);
     }
   };
@@ -366,14 +355,21 @@ __global__ void dequant_kernel(const uint32_t* __restrict__ q, const uint16_t* _
   }
 }
 
+// Column slab width: h columns (gate_up) or output columns (down) of one workgroup.
 template <int MODE>
-int launch_gemm(const GemmParams& p, hipStream_t stream) {
+constexpr int slab_cols() { return kWaves * (MODE == kGateUp ? 32 : 64); }
+
+template <int MODE>
+int launch_gemm(const GemmParams& params, hipStream_t stream) {
+  GemmParams p = params;
   const int total = p.n_shared_chunks + p.max_chunks;
   if (total == 0) return JANUS_MOE_OK;
-  const long grid = (long)ceil_div(total, 8) * 8 * p.nslab;
-  JANUS_REQUIRE(grid < (1l << 31), JANUS_MOE_EINVAL, "grouped GEMM grid too large");
   const bool same_k = p.n_shared_chunks == 0 || p.K_sh == p.K;
   const int nkb = same_k ? p.K / KS : 0;
+  const int out = MODE == kGateUp ? max(p.N, p.N_sh) / 2 : max(p.N, p.N_sh);
+  p.nslab = ceil_div(out, slab_cols<MODE>());
+  const long grid = (long)ceil_div(total, 8) * 8 * p.nslab;
+  JANUS_REQUIRE(grid < (1l << 31), JANUS_MOE_EINVAL, "grouped GEMM grid too large");
   const dim3 g((unsigned)grid), b(kThreads);
   switch (nkb) {
     case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2>), g, b, 0, stream, p); break;
