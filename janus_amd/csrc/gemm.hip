@@ -241,17 +241,28 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
     for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = make_scale(sc[slot][cb]);
 #pragma unroll
     for (int t = 0; t < KS / 32; ++t) {
+      // every row block's fragment is read before the decode, which covers the LDS latency (rows past the chunk hold
+      // copies of its first row, so the reads are defined); only the chunk's row blocks are multiplied. An empty asm
+      // takes the activation fragments together with the decoded weights, so the compiler can neither sink a read into
+      // its row block's branch, next to its first use, nor hoist the wait for the reads above the decode.
+      bf16x8 afrag[kRowBlocks];
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb)
+        afrag[rb] = *reinterpret_cast<const bf16x8*>(base + (16 * rb + nl) * kRowBytes + ((4 * g + t) ^ nl) * 16);
+      __builtin_amdgcn_sched_barrier(0);  // the reads issue before the decode
       bf16x8 bfrag[kColBlocks];
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = decode8(bw[slot][cb][t], scl[cb]);
+      static_assert(kRowBlocks == 6 && kColBlocks == 4, "the asm below lists every fragment");
+      asm volatile(""
+                   : "+v"(afrag[0]), "+v"(afrag[1]), "+v"(afrag[2]), "+v"(afrag[3]), "+v"(afrag[4]), "+v"(afrag[5]),
+                     "+v"(bfrag[0]), "+v"(bfrag[1]), "+v"(bfrag[2]), "+v"(bfrag[3]));
 #pragma unroll
       for (int rb = 0; rb < kRowBlocks; ++rb) {
         if (rb < nrb) {
-          const bf16x8 afrag = *reinterpret_cast<const bf16x8*>(base + (16 * rb + nl) * kRowBytes +
-                                                                ((4 * g + t) ^ nl) * 16);
 #pragma unroll
           for (int cb = 0; cb < kColBlocks; ++cb)
-            acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfrag[cb], afrag, acc[rb][cb], 0, 0, 0);
+            acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfrag[cb], afrag[rb], acc[rb][cb], 0, 0, 0);
         }
       }
     }
