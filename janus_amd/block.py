@@ -31,12 +31,24 @@ class W4A16TopKRouter(nn.Module):
         self._prep, self._prep_key = None, None
 
     def prep(self) -> torch.Tensor:
-        """The route op's split of the weight, rebuilt when the weight changes."""
+        """The route op's split of the weight, built when the module moves to a GPU and rebuilt when the weight
+        changes. A rebuild launches kernels, so it cannot happen inside a graph capture (the split would stay unfilled
+        until the first replay): that case raises."""
         w = self.weight
         key = (w.data_ptr(), w._version, w.device)
         if self._prep_key != key:
+            if w.is_cuda and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("W4A16TopKRouter: the router weight changed (or was never prepared) and a graph "
+                                   "capture is running; run one forward, or move the module to the GPU, first")
             self._prep, self._prep_key = ops.router_prepare(w.detach().contiguous()), key
         return self._prep
+
+    def _apply(self, fn, recurse=True):
+        super()._apply(fn, recurse)
+        self._prep, self._prep_key = None, None
+        if self.weight.is_cuda and not torch.cuda.is_current_stream_capturing():
+            self.prep()  # eagerly, so that a capture that is the first forward finds it ready
+        return self
 
     def forward(self, hidden_states):
         x = hidden_states.reshape(-1, self.hidden_dim)

@@ -17,12 +17,11 @@ struct AlignWorkspace {
 
 AlignWorkspace carve_align(Carver& c, int A, int E);
 
-// sorted_ids [sorted_len] is filled with the sentinel A, then the permutation. Either expert_ids/total (reference tile
-// plan, `tiles` entries) or chunks/num_chunks (runs of at most chunk_rows rows of one expert) may be null. zero_buf, if
-// given, is cleared (zero_len floats, a multiple of 4) by the first launch.
+// sorted_ids [sorted_len] gets the permutation, the sentinel A everywhere else. Either expert_ids/total (reference tile
+// plan, `tiles` entries) or chunks/num_chunks (runs of at most chunk_rows rows of one expert) may be null.
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
-                 float* zero_buf, long zero_len, hipStream_t stream);
+                 hipStream_t stream);
 
 }  // namespace janus

@@ -1,12 +1,13 @@
 // Token-to-expert sort / align / permute on gfx950: a bit-exact integer restatement of align()
-// (janus/moe_w4a16.py:89-106) in three launches, none of which reads back to the host:
-//   1. rank    per block of 1024 assignments: an LDS histogram and the stable rank of every assignment among the
-//              block's assignments of the same expert (wave ballots over the expert-id bits give the peers of each
-//              lane; waves take their turn in assignment order);
-//   2. scan    one workgroup: per-expert totals, per-(block, expert) offsets, padded expert starts, then either the
-//              reference tile plan (expert_ids, total) or the GEMM chunk list;
-//   3. scatter every assignment a lands at start[e] + offset[block][e] + rank[a].
-// The stable order is the assignment id order, exactly as torch.argsort(stable=True) in the reference.
+// (janus/moe_w4a16.py:89-106). The stable order is the assignment id order, exactly as torch.argsort(stable=True) in
+// the reference. Two schedules, chosen by size, with the same results:
+//   small (A <= 65536 assignments: every batch up to 8K tokens at top-8): blocks of 256 assignments, two launches
+//     (rank, place), every block recomputing the per-expert prefix it needs from the blocks' histograms;
+//   large: blocks of 1024 assignments, three launches: rank (an LDS histogram and the stable rank of every assignment
+//     among the block's assignments of the same expert, the block's waves taking their turn in order), scan (one
+//     workgroup: per-expert totals, per-(block, expert) offsets, padded starts), scatter.
+// Within a wave, the peers of a lane (lanes with the same expert id) come from wave ballots over the expert-id bits.
+// Both schedules end with either the reference tile plan (expert_ids, total) or the GEMM chunk list.
 #include "align.h"
 
 namespace janus {
@@ -41,21 +42,178 @@ __device__ int block_inclusive_scan(int v, int* lds_waves /*[16]*/) {
   return r;
 }
 
+// Peers of this lane (the lanes of its wave holding the same valid expert id e; none for e < 0): the lane's stable
+// rank among them, their number and the lowest of them.
+struct Peers {
+  int rank, count, leader;
+};
+__device__ __forceinline__ Peers wave_peers(int e, int nbits) {
+  const int lane = lane_id();
+  uint64_t peers = ballot(e >= 0);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = e >= 0 && ((e >> b) & 1);
+    const uint64_t m = ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  Peers r;
+  r.rank = __popcll(peers & below);
+  r.count = __popcll(peers);
+  r.leader = peers ? (int)__builtin_ctzll(peers) : lane;
+  return r;
+}
+
+// The plan outputs from the inclusive padded cumsum cum[E] (LDS) and the padded starts: reference plan mode
+// (expert_ids != null): expert_ids[i] = #{e : cum[e] <= i*block} (torch.searchsorted right=True), total[0] =
+// cum[E-1]; chunk mode (chunks != null): every expert's rows cut into runs of at most `chunk_rows`. Thread tid < E
+// holds expert tid's count and start. Called by every thread of the workgroup.
+template <typename OutT>
+__device__ void write_plan(const int* cum, int E, int block, int count, int start, OutT* expert_ids, int tiles,
+                           OutT* total_out, int4* chunks, int chunk_rows, int* num_chunks, int* scan_tmp) {
+  const int tid = threadIdx.x, nthreads = blockDim.x;
+  if (expert_ids) {
+    for (int i = tid; i < tiles; i += nthreads) {
+      const long key = (long)i * block;
+      int lo = 0, hi = E;  // first e with cum[e] > key
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if ((long)cum[mid] <= key) lo = mid + 1; else hi = mid;
+      }
+      expert_ids[i] = (OutT)lo;
+    }
+    if (tid == 0) total_out[0] = (OutT)(E > 0 ? cum[E - 1] : 0);
+  }
+  if (chunks) {
+    const int nch = tid < E ? (count + chunk_rows - 1) / chunk_rows : 0;
+    const int incl_ch = block_inclusive_scan(nch, scan_tmp);
+    if (tid < E) {
+      const int first = incl_ch - nch;
+      for (int j = 0; j < nch; ++j)
+        chunks[first + j] = make_int4(tid, start + j * chunk_rows, min(chunk_rows, count - j * chunk_rows), 0);
+      if (tid == E - 1) num_chunks[0] = incl_ch;
+    }
+    if (E == 0 && tid == 0) num_chunks[0] = 0;
+  }
+}
+
+// The small schedule, A <= kSmallMaxA, two launches over blocks of kSmallBlock assignments.
+//   align_small_rank:  per block, each wave's peers (wave ballots), the block's per-expert counts hist[b][e] and the
+//                      rank of every assignment among the block's assignments of the same expert (local_rank);
+//   align_small_place: every block recomputes each expert's total, padded start and the counts of the blocks before
+//                      it from hist (nb <= 256 rows), then places its own assignments at start[e] + (assignments of e
+//                      in earlier blocks) + local_rank; block 0 also writes the sentinel A at every padding position
+//                      and past the last expert, and the plan outputs.
+// No single-workgroup stage: the ranking and the scatter spread over nb workgroups.
+constexpr int kSmallBlock = 256;
+constexpr int kSmallWaves = kSmallBlock / kWave;
+constexpr int kSmallMaxA = kSmallBlock * 256;
+constexpr int kPlaceThreads = 1024;  // one thread per expert (E <= kMaxExperts)
+
+template <typename IdxT>
+__global__ void __launch_bounds__(kSmallBlock) align_small_rank_kernel(const IdxT* __restrict__ idx, int A, int E,
+                                                                       int nbits, int* __restrict__ hist,
+                                                                       int* __restrict__ local_rank) {
+  __shared__ int wcnt[kSmallWaves][kMaxExperts];  // per-wave counts, then per-wave offsets within the block
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  const int a = blockIdx.x * kSmallBlock + tid;
+  int e = -1;
+  if (a < A) {
+    const long v = (long)idx[a];
+    e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are dropped
+  }
+  const Peers pr = wave_peers(e, nbits);
+  for (int i = tid; i < kSmallWaves * kMaxExperts; i += kSmallBlock) (&wcnt[0][0])[i] = 0;
+  __syncthreads();
+  if (e >= 0 && lane == pr.leader) wcnt[wave][e] = pr.count;
+  __syncthreads();
+  for (int x = tid; x < E; x += kSmallBlock) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < kSmallWaves; ++w) {
+      const int h = wcnt[w][x];
+      wcnt[w][x] = c;
+      c += h;
+    }
+    hist[(long)blockIdx.x * E + x] = c;
+  }
+  __syncthreads();
+  if (e >= 0) local_rank[a] = wcnt[wave][e] + pr.rank;
+}
+
+template <typename IdxT, typename OutT>
+__global__ void __launch_bounds__(kPlaceThreads) align_small_place_kernel(
+    const IdxT* __restrict__ idx, int A, int E, int block, int nb, const int* __restrict__ hist,
+    const int* __restrict__ local_rank, OutT* __restrict__ sorted_ids, int sorted_len, OutT* __restrict__ expert_ids,
+    int tiles, OutT* __restrict__ total_out, int4* __restrict__ chunks, int chunk_rows, int* __restrict__ num_chunks) {
+  __shared__ int cum[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int part_count[kPlaceThreads], part_before[kPlaceThreads];
+  __shared__ int scan_tmp[16];
+  const int tid = threadIdx.x, b = blockIdx.x;
+  // Thread g E + x (g < G = kPlaceThreads / E groups) sums hist[j][x] over its blocks j = g mod G, eight loads in
+  // flight at a time: all of the block's threads share the reads, and a read costs a fraction of a memory latency.
+  const int G = kPlaceThreads / E;
+  if (tid < G * E) {
+    const int g = tid / E, x = tid - g * E;
+    int pc = 0, pb = 0;
+    for (int j0 = g; j0 < nb; j0 += 8 * G) {
+      int h[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u * G;
+        h[u] = j < nb ? hist[(long)j * E + x] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        pc += h[u];
+        if (j0 + u * G < b) pb += h[u];
+      }
+    }
+    part_count[tid] = pc;
+    part_before[tid] = pb;
+  }
+  __syncthreads();
+  int count = 0, before = 0;
+  if (tid < E) {
+    for (int g = 0; g < G; ++g) {
+      count += part_count[g * E + tid];
+      before += part_before[g * E + tid];
+    }
+  }
+  const int padded = (count + block - 1) / block * block;
+  const int incl = block_inclusive_scan(tid < E ? padded : 0, scan_tmp);
+  const int start = incl - padded;
+  if (tid < E) {
+    cum[tid] = incl;
+    base[tid] = start + before;
+  }
+  __syncthreads();
+  if (tid < kSmallBlock) {
+    const int a = b * kSmallBlock + tid;
+    if (a < A) {
+      const long v = (long)idx[a];
+      if (v >= 0 && v < E) sorted_ids[base[(int)v] + local_rank[a]] = (OutT)a;
+    }
+  }
+  if (b == 0) {
+    if (tid < E)
+      for (int i = count; i < padded; ++i) sorted_ids[start + i] = (OutT)A;
+    const int total = E > 0 ? cum[E - 1] : 0;
+    for (int i = total + tid; i < sorted_len; i += kPlaceThreads) sorted_ids[i] = (OutT)A;
+    write_plan<OutT>(cum, E, block, count, start, expert_ids, tiles, total_out, chunks, chunk_rows, num_chunks,
+                     scan_tmp);
+  }
+}
+
 template <typename IdxT, typename OutT>
 __global__ void __launch_bounds__(kRankThreads) align_rank_kernel(const IdxT* __restrict__ idx, int A, int E, int nbits,
                                                                   int* __restrict__ hist, int* __restrict__ local_rank,
-                                                                  OutT* __restrict__ sorted_ids, int sorted_len,
-                                                                  float* __restrict__ zero_buf, long zero_len) {
+                                                                  OutT* __restrict__ sorted_ids, int sorted_len) {
   __shared__ int cnt[kMaxExperts];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
-  // Side jobs, grid-stride: fill the output permutation with the sentinel, clear the combine accumulator.
+  // Side job, grid-stride: fill the output permutation with the sentinel.
   for (long i = (long)blockIdx.x * blockDim.x + tid; i < sorted_len; i += (long)gridDim.x * blockDim.x)
     sorted_ids[i] = (OutT)A;
-  if (zero_buf) {
-    float4* z = reinterpret_cast<float4*>(zero_buf);
-    for (long i = (long)blockIdx.x * blockDim.x + tid; i < zero_len / 4; i += (long)gridDim.x * blockDim.x)
-      z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   const int base = blockIdx.x * kAlignChunk;
   if (base >= A) return;
   for (int e = tid; e < E; e += kRankThreads) cnt[e] = 0;
@@ -67,17 +225,8 @@ __global__ void __launch_bounds__(kRankThreads) align_rank_kernel(const IdxT* __
       long v = (long)idx[a];
       e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are dropped
     }
-    // Peers: lanes of this wave holding the same expert id.
-    uint64_t peers = ballot(e >= 0);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = e >= 0 && ((e >> b) & 1);
-      const uint64_t m = ballot(bit);
-      peers &= bit ? m : ~m;
-    }
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-    const int rank_in_wave = __popcll(peers & below);
-    const int n_peers = __popcll(peers);
-    const int leader = peers ? (__ffsll((unsigned long long)peers) - 1) : lane;
+    const Peers pr = wave_peers(e, nbits);
+    const int rank_in_wave = pr.rank, n_peers = pr.count, leader = pr.leader;
     // Waves of this round take their turn in assignment order.
     for (int w = 0; w < kRankThreads / kWave; ++w) {
       if (wave == w) {
@@ -124,30 +273,8 @@ __global__ void __launch_bounds__(kScanThreads) align_scan_kernel(int* __restric
     start[tid] = incl - padded;
   }
   __syncthreads();
-  const int total = cum[E - 1];
-  if (expert_ids) {
-    for (int i = tid; i < tiles; i += kScanThreads) {
-      const long key = (long)i * block;
-      int lo = 0, hi = E;  // first e with cum[e] > key
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if ((long)cum[mid] <= key) lo = mid + 1; else hi = mid;
-      }
-      expert_ids[i] = (OutT)lo;
-    }
-    if (tid == 0) total_out[0] = (OutT)total;
-  }
-  if (chunks) {
-    const int nch = (c + chunk_rows - 1) / chunk_rows;
-    const int incl_ch = block_inclusive_scan(tid < E ? nch : 0, waves);
-    if (tid < E) {
-      const int first = incl_ch - nch;
-      for (int j = 0; j < nch; ++j)
-        chunks[first + j] = make_int4(tid, start[tid] + j * chunk_rows, min(chunk_rows, c - j * chunk_rows), 0);
-      if (tid == E - 1) num_chunks[0] = incl_ch;
-    }
-    if (E == 0 && tid == 0) num_chunks[0] = 0;
-  }
+  write_plan<OutT>(cum, E, block, c, tid < E ? start[tid] : 0, expert_ids, tiles, total_out, chunks, chunk_rows,
+                   num_chunks, waves);
 }
 
 template <typename IdxT, typename OutT>
@@ -177,7 +304,7 @@ int expert_bits(int E) {
 
 AlignWorkspace carve_align(Carver& c, int A, int E) {
   AlignWorkspace w;
-  const int nb = ceil_div(A, kAlignChunk);
+  const int nb = A <= kSmallMaxA ? ceil_div(A, kSmallBlock) : ceil_div(A, kAlignChunk);
   w.hist = c.take<int>((size_t)(nb > 0 ? nb : 1) * E);
   w.local_rank = c.take<int>(A > 0 ? A : 1);
   w.counts = c.take<int>(E);
@@ -188,33 +315,42 @@ AlignWorkspace carve_align(Carver& c, int A, int E) {
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
-                 float* zero_buf, long zero_len, hipStream_t stream) {
+                 hipStream_t stream) {
+  if (A <= kSmallMaxA) {
+    const int nb = ceil_div(A, kSmallBlock);
+    if (nb > 0) {
+      hipLaunchKernelGGL((align_small_rank_kernel<IdxT>), dim3(nb), dim3(kSmallBlock), 0, stream, idx, A, E,
+                         expert_bits(E), w.hist, w.local_rank);
+      JANUS_LAUNCH_CHECK("align_small_rank");
+    }
+    hipLaunchKernelGGL((align_small_place_kernel<IdxT, OutT>), dim3(nb > 0 ? nb : 1), dim3(kPlaceThreads), 0, stream,
+                       idx, A, E, block, nb, w.hist, w.local_rank, sorted_ids, sorted_len, expert_ids, tiles, total,
+                       chunks, chunk_rows, num_chunks);
+    JANUS_LAUNCH_CHECK("align_small_place");
+    return JANUS_MOE_OK;
+  }
   const int nb = ceil_div(A, kAlignChunk);
-  int grid = nb > 0 ? nb : 1;
+  int grid = nb;
   const int fill_blocks = ceil_div(sorted_len, kRankThreads * 8);
   if (fill_blocks > grid) grid = fill_blocks;
-  const long zero_blocks = (zero_len / 4 + kRankThreads * 8 - 1) / (kRankThreads * 8);
-  if (zero_blocks > grid) grid = (int)(zero_blocks < 4096 ? zero_blocks : 4096);
   hipLaunchKernelGGL((align_rank_kernel<IdxT, OutT>), dim3(grid), dim3(kRankThreads), 0, stream, idx, A, E,
-                     expert_bits(E), w.hist, w.local_rank, sorted_ids, sorted_len, zero_buf, zero_len);
+                     expert_bits(E), w.hist, w.local_rank, sorted_ids, sorted_len);
   JANUS_LAUNCH_CHECK("align_rank");
   hipLaunchKernelGGL((align_scan_kernel<OutT>), dim3(1), dim3(kScanThreads), 0, stream, w.hist, nb, E, block, w.counts,
                      w.start, expert_ids, tiles, total, chunks, chunk_rows, num_chunks);
   JANUS_LAUNCH_CHECK("align_scan");
-  if (nb > 0) {
-    hipLaunchKernelGGL((align_scatter_kernel<IdxT, OutT>), dim3(nb), dim3(kRankThreads), 0, stream, idx, A, E, w.hist,
-                       w.local_rank, w.start, sorted_ids);
-    JANUS_LAUNCH_CHECK("align_scatter");
-  }
+  hipLaunchKernelGGL((align_scatter_kernel<IdxT, OutT>), dim3(nb), dim3(kRankThreads), 0, stream, idx, A, E, w.hist,
+                     w.local_rank, w.start, sorted_ids);
+  JANUS_LAUNCH_CHECK("align_scatter");
   return JANUS_MOE_OK;
 }
 
 template int launch_align<int64_t, int64_t>(const int64_t*, int, int, int, const AlignWorkspace&, int64_t*, int,
-                                            int64_t*, int, int64_t*, int4*, int, int*, float*, long, hipStream_t);
+                                            int64_t*, int, int64_t*, int4*, int, int*, hipStream_t);
 template int launch_align<int64_t, int>(const int64_t*, int, int, int, const AlignWorkspace&, int*, int, int*, int,
-                                        int*, int4*, int, int*, float*, long, hipStream_t);
+                                        int*, int4*, int, int*, hipStream_t);
 template int launch_align<int, int>(const int*, int, int, int, const AlignWorkspace&, int*, int, int*, int, int*,
-                                    int4*, int, int*, float*, long, hipStream_t);
+                                    int4*, int, int*, hipStream_t);
 
 }  // namespace janus
 
@@ -243,5 +379,5 @@ extern "C" int janus_moe_align(const int64_t* top_k_index, int S, int top_k, int
   AlignWorkspace w = carve_align(c, (int)A, E);
   const long tiles = (A + (long)E * (block - 1) + block - 1) / block;
   return launch_align<int64_t, int64_t>(top_k_index, (int)A, E, block, w, sorted_ids, (int)(tiles * block), expert_ids,
-                                        (int)tiles, total, nullptr, 0, nullptr, nullptr, 0, (hipStream_t)stream);
+                                        (int)tiles, total, nullptr, 0, nullptr, (hipStream_t)stream);
 }

@@ -80,7 +80,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   const int A = T * top_k;
   mark(1, stream);
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
-                                   kChunkRows, w.num_chunks, nullptr, 0, stream);
+                                   kChunkRows, w.num_chunks, stream);
   if (rc) return rc;
   const bool shared = I_s > 0;
   GemmParams p = {};

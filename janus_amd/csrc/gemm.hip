@@ -285,7 +285,9 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float gv = acc[rb][cb][i], uv = acc[rb][cb + 2][i];
-          hv[i] = gv / (1.0f + __expf(-gv)) * uv;
+          // silu(g) u = g u / (1 + e^-g) with the hardware exp and reciprocal (about 1 ulp each): h is rounded to
+          // bf16 next, which absorbs them; an IEEE division would cost several times the instructions
+          hv[i] = gv * uv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
         }
         uint2 st;
         st.x = pack_bf16x2(hv[0], hv[1]);

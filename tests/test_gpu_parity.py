@@ -63,6 +63,8 @@ def test_dequant_bit_exact_over_codes_and_scales(gpu):
     (0, 2, 8, 16, 0), (1, 1, 1, 16, 0), (5, 2, 8, 16, 0), (40, 2, 8, 16, 1), (96, 8, 256, 16, 0),
     (700, 8, 16, 64, 1), (2048, 8, 256, 64, 0), (2048, 8, 256, 16, 2), (3000, 4, 60, 32, 0),
     (16384, 8, 256, 64, 0), (16384, 8, 256, 128, 2), (1000, 8, 1024, 16, 0),
+    # either side of the small schedule's limit (65536 assignments)
+    (8191, 8, 256, 16, 1), (8192, 8, 64, 16, 2), (65537, 1, 1024, 16, 2),
 ])
 def test_align_bit_exact(gpu, S, k, E, block, skew):
     rng = np.random.default_rng(S * 31 + E)
@@ -199,3 +201,71 @@ def test_block_matches_oracle(gpu, name, sample):
     ref, _, _, _ = O.block_forward(O.numpy_layer(L), bf16_np(x), cfg.k, tokens)
     got = bf16_np(out) if tokens is None else bf16_np(out)[tokens]
     assert_layer_close(got, ref, name)
+
+
+def _replays_match_eager(blk, x, capture_first=False):
+    """A captured forward replayed three times with eager forwards in between: every replay equals the eager output
+    bit for bit (the layer is deterministic). With capture_first the capture is the thread's first block call."""
+    with torch.no_grad():
+        if capture_first:
+            graph, static_out = _capture(blk, x)
+            eager = blk(x).clone()
+        else:
+            eager = blk(x).clone()
+            graph, static_out = _capture(blk, x)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, eager)
+            again = blk(x)  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(again, eager)
+
+
+def _capture(blk, x):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = blk(x)
+    return graph, out
+
+
+def test_block_graph_replay_matches_eager(gpu):
+    """Captured after a warm-up on a side stream, as the reference's LevelGraphs captures, and replayed."""
+    cfg = synth.CONFIGS["short"]
+    _, blk = _block(cfg, gpu)
+    x = synth.activations(cfg).to(gpu)
+    with torch.no_grad():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            blk(x)  # warm-up off the capture stream, as the reference's LevelGraphs does
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+    _replays_match_eager(blk, x)
+
+
+def test_block_graph_captured_first_in_a_fresh_thread(gpu):
+    """The first block call of a fresh thread is the capture itself (torch's per-thread current stream, a new
+    allocator pool); replays still match eager execution."""
+    import threading
+
+    cfg = synth.CONFIGS["short"]
+    _, blk = _block(cfg, gpu)
+    x = synth.activations(cfg).to(gpu)
+    result = {}
+
+    def work():
+        try:
+            torch.cuda.set_device(gpu)
+            _replays_match_eager(blk, x, capture_first=True)
+            result["ok"] = True
+        except BaseException as e:  # reported in the test's thread
+            result["err"] = e
+
+    th = threading.Thread(target=work)
+    th.start()
+    th.join(timeout=120)
+    assert not th.is_alive(), "capture thread did not finish"
+    if "err" in result:
+        raise result["err"]
+    assert result.get("ok")
