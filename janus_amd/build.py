@@ -27,11 +27,8 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-fvisibility=hidden",
-    "-munsafe-fp-atomics",
     # packed fp32 VALU ops stay off: plain fp32 code only
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # no accumulating v_dot2c_f32_bf16: the 3-operand v_dot2_f32_bf16 keeps a shared addend without copies
-    "-Xclang", "-target-feature", "-Xclang", "-dot13-insts",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]
@@ -46,7 +43,7 @@ def hipcc() -> str:
 
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line and "dot13-insts" not in line)
+    out = "\n".join(line for line in proc.stdout.splitlines() if "packed-fp32-ops" not in line)
     if proc.returncode != 0:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
     if out.strip():
