@@ -14,6 +14,10 @@
  *   bf16(float(q) * float(scale)), rounded to nearest even once.
  *   Expert stacks: gate_up words [E, 2I, H/8] (rows 0..I-1 gate, I..2I-1 up), scales [E, 2I, H/128];
  *   down words [E, H, I/8], scales [E, H, I/128].
+ *   NVFP4 weights (the ModelOpt layout janus/hybrid.py loads): e2m1 codes packed two per byte [rows, K/2] uint8
+ *   (low nibble = even k; bit 3 sign, bits 2-1 exponent, bit 0 mantissa), OCP e4m3 block scales [rows, K/16] uint8,
+ *   an fp32 global scale per row [rows]. The weight value is bf16(fp32(e2m1 * fp32(scale * global))): two fp32
+ *   products, then one rounding to bf16, as the reference's dequantise path and fused kernel compute it.
  */
 #ifndef JANUS_MOE_H
 #define JANUS_MOE_H
@@ -98,6 +102,24 @@ JANUS_MOE_API int janus_moe_experts(const uint16_t* x, const int64_t* top_k_inde
                       const int32_t* gate_up_q, const uint16_t* gate_up_s, const int32_t* down_q,
                       const uint16_t* down_s, int S, int H, int I, int E, int top_k, uint16_t* out, void* ws,
                       size_t ws_bytes, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces fused_moe (janus/moe_w4a16.py:122-140) on its own NVFP4 stacks, the reference's arguments one for one:
+ *   gate_up [E, 2I, H/2] uint8, gate_up_scale [E, 2I, H/16] e4m3 bytes, gate_up_global [E, 2I] fp32 (the reference's
+ *   [E, 2I, 1]), down [E, H, I/2], down_scale [E, H, I/16], down_global [E, H]. Same outputs and numerics as
+ *   janus_moe_experts apart from the decode; same workspace (janus_moe_experts_workspace_bytes). */
+JANUS_MOE_API int janus_moe_experts_nvfp4(const uint16_t* x, const int64_t* top_k_index, const float* top_k_weights,
+                                          const uint8_t* gate_up, const uint8_t* gate_up_scale,
+                                          const float* gate_up_global, const uint8_t* down, const uint8_t* down_scale,
+                                          const float* down_global, int S, int H, int I, int E, int top_k,
+                                          uint16_t* out, void* ws, size_t ws_bytes, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces nvfp4_dequantize (janus/hybrid.py:426-437) and with it NVFP4Experts.gate_up_proj / down_proj
+ * (:539-545): out [rows, K] bf16 from packed [rows, K/2] uint8, scale [rows, K/16] e4m3 bytes, global [rows] fp32,
+ * by the device decode the GEMMs use. K % 16 == 0; stacks [E, N, K] are rows = E * N. */
+JANUS_MOE_API int janus_moe_dequant_nvfp4(const uint8_t* packed, const uint8_t* scale, const float* global, long rows,
+                                          int K, uint16_t* out, janus_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------
  * Replaces the dequantising properties NVFP4Experts.gate_up_proj / down_proj and NVFP4Linear.weight

@@ -76,7 +76,8 @@ template <typename IdxT>
 int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const int32_t* guq, const uint16_t* gus,
                 const int32_t* dq, const uint16_t* ds, const int32_t* sguq, const uint16_t* sgus, const int32_t* sdq,
                 const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
-                const ExpertsWorkspace& w, hipStream_t stream) {
+                const ExpertsWorkspace& w, hipStream_t stream, int codec = 0, const float* gu_global = nullptr,
+                const float* dn_global = nullptr) {
   const int A = T * top_k;
   mark(1, stream);
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
@@ -90,12 +91,14 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.T = T;
   p.chunks = w.chunks;
   p.num_chunks = w.num_chunks;
+  p.codec = codec;
   p.max_chunks = w.C;
   p.n_shared_chunks = shared ? ceil_div(T, kChunkRows) : 0;
   // gate_up
   p.a = x;
   p.q = guq;
   p.s = gus;
+  p.gsc = gu_global;
   p.N = 2 * I;
   p.K = H;
   p.q_sh = sguq;
@@ -113,6 +116,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.a_sh = w.h_sh;
   p.q = dq;
   p.s = ds;
+  p.gsc = dn_global;
   p.N = H;
   p.K = I;
   p.q_sh = sdq;
@@ -191,6 +195,39 @@ extern "C" int janus_moe_experts(const uint16_t* x, const int64_t* top_k_index, 
   mark(0, (hipStream_t)stream);
   return run_experts<int64_t>(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s, nullptr, nullptr,
                               nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w, (hipStream_t)stream);
+}
+
+extern "C" int janus_moe_experts_nvfp4(const uint16_t* x, const int64_t* top_k_index, const float* top_k_weights,
+                                       const uint8_t* gate_up, const uint8_t* gate_up_scale, const float* gate_up_global,
+                                       const uint8_t* down, const uint8_t* down_scale, const float* down_global, int S,
+                                       int H, int I, int E, int top_k, uint16_t* out, void* ws, size_t ws_bytes,
+                                       janus_stream_t stream) {
+  int rc = check_expert_sizes("janus_moe_experts_nvfp4", S, H, I, E, top_k);
+  if (rc) return rc;
+  if (S == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(x && top_k_index && top_k_weights && gate_up && gate_up_scale && gate_up_global && down &&
+                    down_scale && down_global && out,
+                JANUS_MOE_EINVAL, "janus_moe_experts_nvfp4: null pointer");
+  const size_t need = janus_moe_experts_workspace_bytes(S, top_k, E, H, I);
+  JANUS_REQUIRE(ws && ws_bytes >= need, JANUS_MOE_EWORKSPACE, "janus_moe_experts_nvfp4: workspace %zu < %zu bytes",
+                ws_bytes, need);
+  Carver c(ws);
+  ExpertsWorkspace w = carve_experts(c, S, top_k, E, H, I, 0);
+  mark(0, (hipStream_t)stream);
+  return run_experts<int64_t>(x, top_k_index, top_k_weights, reinterpret_cast<const int32_t*>(gate_up),
+                              reinterpret_cast<const uint16_t*>(gate_up_scale),
+                              reinterpret_cast<const int32_t*>(down), reinterpret_cast<const uint16_t*>(down_scale),
+                              nullptr, nullptr, nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w,
+                              (hipStream_t)stream, /*codec=*/1, gate_up_global, down_global);
+}
+
+extern "C" int janus_moe_dequant_nvfp4(const uint8_t* packed, const uint8_t* scale, const float* global, long rows,
+                                       int K, uint16_t* out, janus_stream_t stream) {
+  JANUS_REQUIRE(rows >= 0 && K > 0 && K % 16 == 0, JANUS_MOE_EINVAL,
+                "janus_moe_dequant_nvfp4: rows=%ld K=%d (need K %% 16 == 0)", rows, K);
+  if (rows == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(packed && scale && global && out, JANUS_MOE_EINVAL, "janus_moe_dequant_nvfp4: null pointer");
+  return launch_dequant_nvfp4(packed, scale, global, rows, K, out, (hipStream_t)stream);
 }
 
 extern "C" size_t janus_moe_block_workspace_bytes(int T, int H, int I, int E, int top_k, int I_s) {

@@ -19,8 +19,11 @@ struct GemmParams {
   const uint16_t* a_sh;       // down: h of the shared expert [T, K_sh]
   const int* sorted_ids;      // assignment id at each permuted position (< A on real rows)
   int topk, A, T;
-  const int32_t* q;           // routed weight words [E, N, K/8]
-  const uint16_t* s;          // routed scales [E, N, K/128]
+  int codec;                  // 0: int4 group-128 (q words, s bf16 [E, N, K/128]); 1: NVFP4 (q bytes, s e4m3
+                              // [E, N, K/16], gsc fp32 [E, N]); the shared expert is int4 only
+  const int32_t* q;           // routed weight words [E, N, K/8] (NVFP4: the same bytes, [E, N, K/2] uint8)
+  const uint16_t* s;          // routed scales (bytes of the codec's scale layout)
+  const float* gsc;           // NVFP4: global scale per routed weight row [E, N]
   int N, K;                   // routed weight rows and reduction length
   const int32_t* q_sh;        // shared expert [N_sh, K_sh/8], null = none
   const uint16_t* s_sh;
@@ -43,5 +46,7 @@ int launch_down(const GemmParams& p, hipStream_t stream);
 // out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32.
 int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, hipStream_t stream);
 int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream);
+int launch_dequant_nvfp4(const uint8_t* q, const uint8_t* s, const float* gs, long rows, int K, uint16_t* out,
+                         hipStream_t stream);
 
 }  // namespace janus

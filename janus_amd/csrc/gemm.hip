@@ -119,10 +119,57 @@ __device__ __forceinline__ bf16x8 decode8(uint32_t w, const Scale& s) {
 }
 __device__ __forceinline__ bf16x8 decode8(uint32_t w, uint32_t sb) { return decode8(w, make_scale(sb)); }
 
+// NVFP4 (janus/hybrid.py:400-423, janus/moe_w4a16.py:19-33, 68-72): byte b of the word holds elements 2b (low nibble)
+// and 2b + 1 (high nibble) as e2m1 codes, the same k order as the int4 words. W = bf16(fp32(e2m1 * S)) with
+// S = fp32(e4m3 block scale * fp32 global scale of the row): the reference's two fp32 products, then one rounding to
+// bf16. v_cvt_scalef32_pk_f32_fp4 widens the two codes of a byte exactly (scale 1); 16 VALU per word.
+__device__ __forceinline__ bf16x8 decode8_nvfp4(uint32_t w, float S) {
+  const float2_t v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+  const float2_t v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+  const float2_t v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+  const float2_t v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+  const float v[8] = {v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = static_cast<__bf16>(v[j] * S);
+  return r;
+}
+// S of an e4m3 block-scale byte (OCP e4m3fn, as gfx950's fp8 conversions read it) and the row's global scale.
+__device__ __forceinline__ float nvfp4_block_scale(uint32_t e4m3_byte, float global) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)e4m3_byte, 0) * global;
+}
+
+// Per-codec scale state of one column block for one 128-k stage, and the decode of its word t.
+//   int4 group-128: one bf16 scale per stage (2 bytes per row).
+//   NVFP4: two e4m3 block scales per lane (the lane's words t = 0, 1 fall in block 2g, t = 2, 3 in block 2g + 1; the
+//   lane loads the two bytes at 2g of the row's eight per stage) times the row's global scale.
+enum { kInt4 = 0, kNvfp4 = 1 };
+template <int CODEC>
+struct Codec;
+template <>
+struct Codec<kInt4> {
+  static constexpr int kScaleBytesPerStage = 2;  // per row
+  using State = Scale;
+  __device__ static State make(uint32_t sc, float) { return make_scale(sc); }
+  __device__ static bf16x8 decode(uint32_t w, const State& s, int) { return decode8(w, s); }
+};
+template <>
+struct Codec<kNvfp4> {
+  static constexpr int kScaleBytesPerStage = 8;
+  struct State {
+    float s0, s1;
+  };
+  __device__ static State make(uint32_t sc, float global) {
+    return State{nvfp4_block_scale(sc & 0xFFu, global), nvfp4_block_scale((sc >> 8) & 0xFFu, global)};
+  }
+  __device__ static bf16x8 decode(uint32_t w, const State& s, int t) { return decode8_nvfp4(w, t < 2 ? s.s0 : s.s1); }
+};
+
 // NKB: k stages (K / 128) fixed at compile time, the whole k loop unrolled so the compiler's wait counts for the
 // weight registers are exact (a runtime loop makes it wait for every outstanding load); 0 = runtime K.
-template <int MODE, int NKB>
+template <int MODE, int NKB, int CODEC>
 __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
+  using C = Codec<CODEC>;
   // LDS double buffer of activation tiles, [buffer][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16
   // lanes of a fragment read (same chunk, 16 rows) hit 16 different bank groups.
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
@@ -138,12 +185,13 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
   const bool shared = c < p.n_shared_chunks;
   int pos0, rows, N, K;
   const int32_t* wq;
-  const uint16_t* wsc;
+  const unsigned char* wsc;
+  const float* wgl = nullptr;  // NVFP4: global scale of each weight row
   if (shared) {
     pos0 = c * kChunkRows;
     rows = min(kChunkRows, p.T - pos0);
     wq = p.q_sh;
-    wsc = p.s_sh;
+    wsc = reinterpret_cast<const unsigned char*>(p.s_sh);
     N = p.N_sh;
     K = p.K_sh;
   } else {
@@ -155,7 +203,8 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
     N = p.N;
     K = p.K;
     wq = p.q + (long)ch.x * N * (K / 8);
-    wsc = p.s + (long)ch.x * N * (K / 128);
+    wsc = reinterpret_cast<const unsigned char*>(p.s) + (long)ch.x * N * (K / KS) * C::kScaleBytesPerStage;
+    if (CODEC == kNvfp4) wgl = p.gsc + (long)ch.x * N;
   }
   constexpr int kWaveCols = (MODE == kGateUp) ? 32 : 64;  // h columns (gate_up) or output columns (down)
   const int out_cols = (MODE == kGateUp) ? N / 2 : N;
@@ -188,8 +237,9 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
 
   // ---- weight rows of this lane, one per column block (an idle wave reads row 0 and discards it) ----
   const unsigned char* wbase = reinterpret_cast<const unsigned char*>(wq);
-  const unsigned char* sbase = reinterpret_cast<const unsigned char*>(wsc);
+  const unsigned char* sbase = wsc;
   uint32_t woff[kColBlocks], soff[kColBlocks];
+  float gq[kColBlocks];
 #pragma unroll
   for (int cb = 0; cb < kColBlocks; ++cb) {
     int n;
@@ -199,7 +249,8 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
       n = col0 + 16 * cb + nl;
     if (!active) n = 0;
     woff[cb] = (uint32_t)n * (uint32_t)(K / 2) + g * 16;
-    soff[cb] = (uint32_t)n * (uint32_t)(K / 64);
+    soff[cb] = (uint32_t)n * (uint32_t)(K / KS * C::kScaleBytesPerStage) + (CODEC == kNvfp4 ? g * 2 : 0);
+    gq[cb] = CODEC == kNvfp4 ? wgl[n] : 0.0f;
   }
 
   f32x4 acc[kRowBlocks][kColBlocks];
@@ -230,15 +281,15 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
       bw[slot][cb] = *reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2));
-      sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * 2);
+      sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
     }
   };
   auto compute = [&](auto slot_c, int buf) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
     const unsigned char* base = lds + buf * kSlotBytes;
-    Scale scl[kColBlocks];
+    typename C::State scl[kColBlocks];
 #pragma unroll
-    for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = make_scale(sc[slot][cb]);
+    for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = C::make(sc[slot][cb], gq[cb]);
 #pragma unroll
     for (int t = 0; t < KS / 32; ++t) {
       // every row block's fragment is read before the decode, which covers the LDS latency (rows past the chunk hold
@@ -252,7 +303,7 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
       __builtin_amdgcn_sched_barrier(0);  // the reads issue before the decode
       bf16x8 bfrag[kColBlocks];
 #pragma unroll
-      for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = decode8(bw[slot][cb][t], scl[cb]);
+      for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = C::decode(bw[slot][cb][t], scl[cb], t);
       static_assert(kRowBlocks == 6 && kColBlocks == 4, "the asm below lists every fragment");
       asm volatile(""
                    : "+v"(afrag[0]), "+v"(afrag[1]), "+v"(afrag[2]), "+v"(afrag[3]), "+v"(afrag[4]), "+v"(afrag[5]),
@@ -368,6 +419,18 @@ __global__ void dequant_kernel(const uint32_t* __restrict__ q, const uint16_t* _
   }
 }
 
+// bf16 weights of an NVFP4 matrix [rows, K]: packed e2m1 bytes [rows, K/2] (as int32 words), e4m3 block scales
+// [rows, K/16], fp32 global scale per row [rows] (janus/hybrid.py:415-423, the dequantise path's values).
+__global__ void dequant_nvfp4_kernel(const uint32_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                     const float* __restrict__ gs, long rows, int K, bf16x8* __restrict__ out) {
+  const long words = rows * (K / 8);
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / (K / 8);
+    const int j = (int)(i % (K / 8));
+    out[i] = decode8_nvfp4(q[i], nvfp4_block_scale(s[r * (K / 16) + j / 2], gs[r]));
+  }
+}
+
 // Column slab width: h columns (gate_up) or output columns (down) of one workgroup.
 template <int MODE>
 constexpr int slab_cols() { return kWaves * (MODE == kGateUp ? 32 : 64); }
@@ -384,13 +447,22 @@ int launch_gemm(const GemmParams& params, hipStream_t stream) {
   const long grid = (long)ceil_div(total, 8) * 8 * p.nslab;
   JANUS_REQUIRE(grid < (1l << 31), JANUS_MOE_EINVAL, "grouped GEMM grid too large");
   const dim3 g((unsigned)grid), b(kThreads);
-  switch (nkb) {
-    case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2>), g, b, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 4>), g, b, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 8>), g, b, 0, stream, p); break;
-    case 16: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 16>), g, b, 0, stream, p); break;
-    default: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 0>), g, b, 0, stream, p); break;
+  JANUS_REQUIRE(p.codec == kInt4 || (p.codec == kNvfp4 && p.gsc && p.n_shared_chunks == 0), JANUS_MOE_EINVAL,
+                "grouped GEMM: codec %d (NVFP4 needs global scales and no shared chunks)", p.codec);
+#define JANUS_GEMM_CASES(CODEC)                                                                          \
+  switch (nkb) {                                                                                        \
+    case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2, CODEC>), g, b, 0, stream, p); break;         \
+    case 4: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 4, CODEC>), g, b, 0, stream, p); break;         \
+    case 8: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 8, CODEC>), g, b, 0, stream, p); break;         \
+    case 16: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 16, CODEC>), g, b, 0, stream, p); break;       \
+    default: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 0, CODEC>), g, b, 0, stream, p); break;        \
   }
+  if (p.codec == kNvfp4) {
+    JANUS_GEMM_CASES(kNvfp4)
+  } else {
+    JANUS_GEMM_CASES(kInt4)
+  }
+#undef JANUS_GEMM_CASES
   JANUS_LAUNCH_CHECK(MODE == kGateUp ? "w4a16 gate_up" : "w4a16 down");
   return JANUS_MOE_OK;
 }
@@ -408,6 +480,18 @@ int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, 
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, reinterpret_cast<const float4*>(slots),
                      nslots, reinterpret_cast<uint2*>(out), T, H / 4);
   JANUS_LAUNCH_CHECK("combine");
+  return JANUS_MOE_OK;
+}
+
+int launch_dequant_nvfp4(const uint8_t* q, const uint8_t* s, const float* gs, long rows, int K, uint16_t* out,
+                         hipStream_t stream) {
+  const long words = rows * (K / 8);
+  if (words == 0) return JANUS_MOE_OK;
+  long blocks = (words + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  hipLaunchKernelGGL(dequant_nvfp4_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<const uint32_t*>(q), s, gs, rows, K, reinterpret_cast<bf16x8*>(out));
+  JANUS_LAUNCH_CHECK("dequant_nvfp4");
   return JANUS_MOE_OK;
 }
 

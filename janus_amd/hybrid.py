@@ -1,6 +1,8 @@
-"""The MoE slice of janus/hybrid.py (:395-701) for the int4 group-128 codec: the codec, `W4A16Linear` (the
-NVFP4Linear counterpart), `W4A16Experts` (the NVFP4Experts counterpart, same forward signature and attributes) and
-`moe_kernel` (the JANUS_MOE_KERNEL switch).
+"""The MoE slice of janus/hybrid.py (:395-701): two weight codecs and their modules, and `moe_kernel` (the
+JANUS_MOE_KERNEL switch).
+  - int4 group-128 (this port's headline codec): `W4A16Linear`, `W4A16Experts`.
+  - NVFP4 (the reference's ModelOpt checkpoint format, janus/hybrid.py:395-451): `nvfp4_quantize` /
+    `nvfp4_dequantize`, `NVFP4Linear`, `NVFP4Experts`, same names, buffers and forward signatures as the reference.
 
 Dispatch follows janus/hybrid.py:551-572: under inference on a GPU the experts run the fused HIP kernels
 (`moe_w4a16.fused_moe`); with gradients enabled or on the CPU the stacks are dequantised per call and run through
@@ -60,6 +62,71 @@ def int4_quantize(w: torch.Tensor, group: int = GROUP) -> tuple[torch.Tensor, to
     return int4_pack(q), s
 
 
+# ---- NVFP4 codec (janus/hybrid.py:400-451) --------------------------------------------------------------------
+
+FP4_BLOCK = 16
+FP4_MAX = 6.0    # e2m1's largest magnitude
+FP8_MAX = 448.0  # e4m3fn's largest finite value
+_E2M1 = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)  # codes 0..7; bit 3 is the sign
+
+
+def _e2m1_decode(codes: torch.Tensor) -> torch.Tensor:
+    """uint8 e2m1 codes (0..15) -> fp32 (bit 3 sign, bits 2-1 exponent, bit 0 mantissa; 8 is -0)."""
+    table = torch.tensor(_E2M1, dtype=torch.float32, device=codes.device)
+    mag = table[(codes & 7).long()]
+    return torch.where((codes & 8) != 0, -mag, mag)
+
+
+def _e2m1_encode(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> uint8 e2m1 codes, nearest with ties to even (ModelOpt's rule): a magnitude goes to the code above a
+    midpoint between neighbouring values, and exactly at a midpoint to the neighbour with an even code."""
+    mag = x.abs()
+    code = torch.zeros_like(mag, dtype=torch.uint8)
+    for c in range(1, 8):
+        mid = (_E2M1[c - 1] + _E2M1[c]) / 2
+        up = mag >= mid if c % 2 == 0 else mag > mid
+        code = torch.where(up, torch.full_like(code, c), code)
+    return code | ((x < 0).to(torch.uint8) << 3)
+
+
+def _rows_global(global_scale: torch.Tensor, lead: tuple) -> torch.Tensor:
+    """A global scale given as a scalar, [..., 1] or [...] -> fp32 [...] over the leading (row) dimensions."""
+    g = global_scale.float()
+    if g.dim() and g.shape[-1] == 1 and g.dim() == len(lead) + 1:
+        g = g.squeeze(-1)
+    return g.expand(lead).contiguous() if g.dim() == 0 else g.reshape(lead).contiguous()
+
+
+def nvfp4_dequantize(packed: torch.Tensor, scale: torch.Tensor, global_scale: torch.Tensor,
+                     dtype=torch.bfloat16) -> torch.Tensor:
+    """ModelOpt NVFP4 (packed [..., K/2] uint8, low nibble = even k; e4m3 block scales [..., K/16]; fp32 global as a
+    scalar, [..., 1] or [...]) -> `dtype` [..., K] = dtype(fp32(e2m1 * fp32(scale * global))): the reference's two fp32
+    products (janus/hybrid.py:415-423), then one rounding. bf16 on a GPU runs the HIP decode the GEMMs use."""
+    lead = tuple(packed.shape[:-1])
+    if packed.is_cuda and dtype == torch.bfloat16:
+        from . import ops
+        return ops.dequant_nvfp4(packed.contiguous(), scale.contiguous(), _rows_global(global_scale, lead))
+    codes = torch.stack([packed & 15, packed >> 4], dim=-1).flatten(-2)
+    s = scale.float() * _rows_global(global_scale, lead)[..., None]
+    values = _e2m1_decode(codes).view(*lead, -1, FP4_BLOCK) * s[..., None]
+    return values.reshape(codes.shape).to(dtype)
+
+
+def nvfp4_quantize(w: torch.Tensor, global_scale: torch.Tensor | None = None):
+    """A float weight [..., K] (K a multiple of 16) -> (packed uint8 [..., K/2], e4m3 block scales [..., K/16], fp32
+    global scalar), ModelOpt's recipe as the reference applies it (janus/hybrid.py:440-451): global = amax / (6 * 448)
+    so every block scale fits e4m3, block scale = e4m3(block amax / 6 / global) (1 for an all-zero block), codes =
+    nearest-even e2m1 of w / (block scale * global)."""
+    w = w.float()
+    if global_scale is None:
+        global_scale = (w.abs().amax() / (FP4_MAX * FP8_MAX)).clamp(min=torch.finfo(torch.float32).tiny)
+    blocks = w.view(*w.shape[:-1], -1, FP4_BLOCK)
+    bscale = blocks.abs().amax(-1) / FP4_MAX / global_scale
+    bscale = torch.where(bscale == 0, torch.ones_like(bscale), bscale).to(torch.float8_e4m3fn)
+    codes = _e2m1_encode(blocks / (bscale.float() * global_scale)[..., None]).reshape(w.shape)
+    return (codes[..., ::2] | (codes[..., 1::2] << 4)).contiguous(), bscale, global_scale.reshape(())
+
+
 # ---- modules -------------------------------------------------------------------------------------------------
 
 def moe_kernel(device) -> str:
@@ -95,38 +162,45 @@ class W4A16Linear(nn.Module):
         return F.linear(x, self.weight.to(x.dtype))
 
 
-class W4A16Experts(nn.Module):
-    """The expert stack of a sparse MoE block (`gate_up_proj [E, 2I, H]`, `down_proj [E, H, I]`) held packed:
-    gate_up [E, 2I, H/8] int32 (rows 0..I-1 gate, I..2I-1 up), gate_up_scale [E, 2I, H/128] bf16, down [E, H, I/8],
-    down_scale [E, H, I/128]. The `*_global` buffers exist for fused_moe's reference arity (ones; the codec has no
-    global scale). forward has the HF experts' signature (janus/hybrid.py:512-618)."""
+class NVFP4Linear(nn.Module):
+    """A bias-free linear whose weight stays packed as ModelOpt NVFP4 (uint8 pairs, e4m3 per-16 block scales, an fp32
+    global scale; 0.56 bytes per weight) and is dequantised at every call (janus/hybrid.py:483-509, the fp4=False
+    mode). The fp4 tensor-core mode (`fp4=True`) quantises the activations to fp4, which is not W4A16; it is not built
+    here and asking for it raises. Buffers only."""
 
-    def __init__(self, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global, act_fn=F.silu):
+    def __init__(self, packed: torch.Tensor, scale: torch.Tensor, global_scale: torch.Tensor):
         super().__init__()
-        E = gate_up.shape[0]
-        if gate_up_global is None:
-            gate_up_global = torch.ones(E, gate_up.shape[1], 1, device=gate_up.device)
-        if down_global is None:
-            down_global = torch.ones(E, down.shape[1], 1, device=down.device)
-        for name, t in (("gate_up", gate_up), ("gate_up_scale", gate_up_scale), ("gate_up_global", gate_up_global),
-                        ("down", down), ("down_scale", down_scale), ("down_global", down_global)):
-            self.register_buffer(name, t, persistent=False)
-        self.num_experts, self.hidden_dim, self.intermediate_dim = E, gate_up.shape[2] * 8, down.shape[2] * 8
-        self.act_fn, self.has_gate, self.has_bias, self.is_transposed = act_fn, True, False, False
-        self.fused, self.blocked = None, None
+        self.register_buffer("packed", packed, persistent=False)
+        self.register_buffer("scale", scale, persistent=False)
+        self.register_buffer("global_scale", global_scale.reshape(()).float(), persistent=False)
+        self.blocked, self.fused = None, None
+        self.in_features, self.out_features = packed.shape[1] * 2, packed.shape[0]
 
     def set_mode(self, fp4, fused=None):
         if fp4:
-            raise ValueError("fp4 tensor-core mode needs NVFP4 weights; the int4 codec has none")
+            raise ValueError("fp4 tensor-core mode (fp4 activations) is not part of the W4A16 path")
         self.fused = fused
 
     @property
-    def gate_up_proj(self) -> torch.Tensor:
-        return int4_dequantize(self.gate_up, self.gate_up_scale, torch.bfloat16)
+    def weight(self) -> torch.Tensor:
+        return nvfp4_dequantize(self.packed, self.scale, self.global_scale, torch.bfloat16)
 
-    @property
-    def down_proj(self) -> torch.Tensor:
-        return int4_dequantize(self.down, self.down_scale, torch.bfloat16)
+    def forward(self, x):
+        return F.linear(x, self.weight.to(x.dtype))
+
+
+class _PackedExperts(nn.Module):
+    """The expert-stack behaviour shared by both codecs (janus/hybrid.py:512-618): forward with the HF experts'
+    signature, dispatched by `moe_kernel` to the fused HIP kernels or to a dequantise-per-call torch path."""
+
+    def _set_buffers(self, **tensors):
+        for name, t in tensors.items():
+            self.register_buffer(name, t, persistent=False)
+
+    def set_mode(self, fp4, fused=None):
+        if fp4:
+            raise ValueError("fp4 tensor-core mode (fp4 activations) is not part of the W4A16 path")
+        self.fused = fused
 
     def _apply_gate(self, gate_up_out):
         gate, up = gate_up_out.chunk(2, dim=-1)
@@ -205,3 +279,55 @@ class W4A16Experts(nn.Module):
             y = F.linear(h, down[e].to(x.dtype))
             out.index_add_(0, token, (y * top_k_weights[token, slot, None]).to(out.dtype))
         return out
+
+
+class W4A16Experts(_PackedExperts):
+    """The expert stack of a sparse MoE block (`gate_up_proj [E, 2I, H]`, `down_proj [E, H, I]`) held packed in the
+    int4 group-128 codec: gate_up [E, 2I, H/8] int32 (rows 0..I-1 gate, I..2I-1 up), gate_up_scale [E, 2I, H/128]
+    bf16, down [E, H, I/8], down_scale [E, H, I/128]. The `*_global` buffers exist for fused_moe's reference arity
+    (ones; the codec has no global scale). forward has the HF experts' signature (janus/hybrid.py:512-618)."""
+
+    def __init__(self, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global, act_fn=F.silu):
+        super().__init__()
+        E = gate_up.shape[0]
+        if gate_up_global is None:
+            gate_up_global = torch.ones(E, gate_up.shape[1], 1, device=gate_up.device)
+        if down_global is None:
+            down_global = torch.ones(E, down.shape[1], 1, device=down.device)
+        self._set_buffers(gate_up=gate_up, gate_up_scale=gate_up_scale, gate_up_global=gate_up_global, down=down,
+                          down_scale=down_scale, down_global=down_global)
+        self.num_experts, self.hidden_dim, self.intermediate_dim = E, gate_up.shape[2] * 8, down.shape[2] * 8
+        self.act_fn, self.has_gate, self.has_bias, self.is_transposed = act_fn, True, False, False
+        self.fused, self.blocked = None, None
+
+    @property
+    def gate_up_proj(self) -> torch.Tensor:
+        return int4_dequantize(self.gate_up, self.gate_up_scale, torch.bfloat16)
+
+    @property
+    def down_proj(self) -> torch.Tensor:
+        return int4_dequantize(self.down, self.down_scale, torch.bfloat16)
+
+
+class NVFP4Experts(_PackedExperts):
+    """The reference's NVFP4Experts (janus/hybrid.py:512-618): gate_up [E, 2I, H/2] uint8, gate_up_scale
+    [E, 2I, H/16] e4m3, gate_up_global [E, 2I, 1] fp32 (one value per expert and projection, expanded over rows),
+    down [E, H, I/2], down_scale [E, H, I/16], down_global [E, H, 1]. Buffers only, nothing persisted; the fused path
+    runs the NVFP4 decode inside the HIP GEMMs."""
+
+    def __init__(self, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global, act_fn=F.silu):
+        super().__init__()
+        self._set_buffers(gate_up=gate_up, gate_up_scale=gate_up_scale, gate_up_global=gate_up_global, down=down,
+                          down_scale=down_scale, down_global=down_global)
+        self.num_experts = gate_up.shape[0]
+        self.hidden_dim, self.intermediate_dim = gate_up.shape[2] * 2, down.shape[2] * 2
+        self.act_fn, self.has_gate, self.has_bias, self.is_transposed = act_fn, True, False, False
+        self.fused, self.blocked = None, None
+
+    @property
+    def gate_up_proj(self) -> torch.Tensor:
+        return nvfp4_dequantize(self.gate_up, self.gate_up_scale, self.gate_up_global, torch.bfloat16)
+
+    @property
+    def down_proj(self) -> torch.Tensor:
+        return nvfp4_dequantize(self.down, self.down_scale, self.down_global, torch.bfloat16)

@@ -1,10 +1,13 @@
 """Drop-in for janus/moe_w4a16.py on MI355X: the same `align` and `fused_moe` entry points, backed by the gfx950 HIP
 kernels of libjanus_moe_hip.so through the `janus_moe` custom ops.
 
-Weights use the int4 group-128 codec (int32 words packing 8 two's-complement nibbles along K, bf16 scales per 128
-k; see include/janus_moe.h): `gate_up` [E, 2I, H/8], `gate_up_scale` [E, 2I, H/128], `down` [E, H, I/8],
-`down_scale` [E, H, I/128]. The `*_global` arguments of the reference signature are kept for arity; the int4 codec
-has no global scale, so they must be None or ones (not checked on the device, which would need a sync).
+Two weight codecs, told apart by the stack's dtype (see include/janus_moe.h):
+  - NVFP4, the reference's own arguments: `gate_up` [E, 2I, H/2] uint8, `gate_up_scale` [E, 2I, H/16] e4m3,
+    `gate_up_global` [E, 2I, 1] fp32, `down` [E, H, I/2], `down_scale` [E, H, I/16], `down_global` [E, H, 1];
+  - int4 group-128 (int32 words packing 8 two's-complement nibbles along K, bf16 scales per 128 k): `gate_up`
+    [E, 2I, H/8], `gate_up_scale` [E, 2I, H/128], `down` [E, H, I/8], `down_scale` [E, H, I/128]. This codec has no
+    global scale, so the `*_global` arguments must be None or ones (not checked on the device, which would need a
+    sync).
 
 Numerics differ from the reference kernel in one deliberate way: the routing weights stay fp32 and the weighted sum
 over the top-k runs in fp32 with a single rounding to the output dtype (the reference rounds each expert's output
@@ -34,6 +37,20 @@ def fused_moe(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_glo
     the kernels rebuild their own tile plan from top_k_index on the device."""
     if plan is not None and len(plan) != 3:
         raise ValueError("plan must be align()'s (sorted_ids, expert_ids, total)")
+    if gate_up.dtype == torch.uint8:  # NVFP4
+        S, H = x.shape
+        E, two_i, h2 = gate_up.shape
+        if h2 * 2 != H or H % 128 or (two_i // 2) % 128 or down.shape[2] * 2 != two_i // 2:
+            raise AssertionError((tuple(gate_up.shape), tuple(down.shape), H))
+        if gate_up_global is None or down_global is None:
+            raise ValueError("NVFP4 stacks need their global scales")
+        dtype = x.dtype
+        out = ops.experts_nvfp4(x.to(torch.bfloat16).contiguous(), top_k_index.to(torch.int64).contiguous(),
+                                top_k_weights.to(torch.float32).contiguous(), gate_up.contiguous(),
+                                gate_up_scale.contiguous(), gate_up_global.float().reshape(E, two_i).contiguous(),
+                                down.contiguous(), down_scale.contiguous(),
+                                down_global.float().reshape(E, H).contiguous())
+        return out.to(dtype)
     for name, g in (("gate_up_global", gate_up_global), ("down_global", down_global)):
         if g is not None and not g.is_cuda and not torch.all(g == 1):
             raise ValueError(f"{name}: the int4 group-128 codec has no global scale (expected None or ones)")

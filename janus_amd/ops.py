@@ -129,6 +129,34 @@ def _(words, scales):
     return words.new_empty(*words.shape[:-1], words.shape[-1] * 8, dtype=torch.bfloat16)
 
 
+@torch.library.custom_op("janus_moe::dequant_nvfp4", mutates_args=())
+def dequant_nvfp4(packed: Tensor, scale: Tensor, global_scale: Tensor) -> Tensor:
+    """NVFP4 matrix or stack (packed [..., K/2] uint8, e4m3 scale [..., K/16] (float8_e4m3fn or its uint8 bytes),
+    global [...] or [..., 1] fp32) -> bf16 [..., K] = bf16(fp32(e2m1 * fp32(scale * global))), by the decode the
+    GEMMs use."""
+    dev = _require_gpu(packed, scale, global_scale)
+    K = packed.shape[-1] * 2
+    lead = tuple(packed.shape[:-1])
+    rows = packed.numel() // max(packed.shape[-1], 1)
+    if K % 16:
+        raise ValueError(f"NVFP4: K={K} must be a multiple of 16")
+    _expect(packed, "packed", torch.uint8, tuple(packed.shape))
+    sb = scale.view(torch.uint8) if scale.dtype == torch.float8_e4m3fn else scale
+    _expect(sb, "scale", torch.uint8, (*lead, K // 16))
+    g = global_scale.reshape(lead)
+    _expect(g, "global_scale", torch.float32, lead)
+    out = torch.empty(*lead, K, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().janus_moe_dequant_nvfp4(_ptr(packed), _ptr(sb), _ptr(g), rows, K, _ptr(out), _stream(dev)),
+              "janus_moe_dequant_nvfp4")
+    return out
+
+
+@dequant_nvfp4.register_fake
+def _(packed, scale, global_scale):
+    return packed.new_empty(*packed.shape[:-1], packed.shape[-1] * 2, dtype=torch.bfloat16)
+
+
 # ---- align ---------------------------------------------------------------------------------------------------
 
 def align_shapes(S: int, k: int, num_experts: int, block: int) -> int:
@@ -198,6 +226,47 @@ def experts(x: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up_q: Te
 
 @experts.register_fake
 def _(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("janus_moe::experts_nvfp4", mutates_args=())
+def experts_nvfp4(x: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up: Tensor, gate_up_scale: Tensor,
+                  gate_up_global: Tensor, down: Tensor, down_scale: Tensor, down_global: Tensor) -> Tensor:
+    """Routed experts on NVFP4 stacks (the reference's fused_moe arguments, janus/moe_w4a16.py:122-140) with the fp32
+    weighted combine: [S, H] bf16. Scales may be float8_e4m3fn or their uint8 bytes; globals [E, N] or [E, N, 1]."""
+    dev = _require_gpu(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, down, down_scale,
+                       down_global)
+    S, H = x.shape
+    k = top_k_index.shape[1]
+    E, two_i, h2 = gate_up.shape
+    I = two_i // 2
+    if h2 * 2 != H:
+        raise ValueError(f"gate_up packs K={h2 * 2}, x has H={H}")
+    gus = gate_up_scale.view(torch.uint8) if gate_up_scale.dtype == torch.float8_e4m3fn else gate_up_scale
+    dns = down_scale.view(torch.uint8) if down_scale.dtype == torch.float8_e4m3fn else down_scale
+    gug, dng = gate_up_global.reshape(E, 2 * I), down_global.reshape(E, H)
+    _expect(x, "x", torch.bfloat16, (S, H))
+    _expect(top_k_index, "top_k_index", torch.int64, (S, k))
+    _expect(top_k_weights, "top_k_weights", torch.float32, (S, k))
+    _expect(gate_up, "gate_up", torch.uint8, (E, 2 * I, H // 2))
+    _expect(gus, "gate_up_scale", torch.uint8, (E, 2 * I, H // 16))
+    _expect(gug, "gate_up_global", torch.float32, (E, 2 * I))
+    _expect(down, "down", torch.uint8, (E, H, I // 2))
+    _expect(dns, "down_scale", torch.uint8, (E, H, I // 16))
+    _expect(dng, "down_global", torch.float32, (E, H))
+    out = torch.empty(S, H, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    n = L.janus_moe_experts_workspace_bytes(S, k, E, H, I)
+    ws = _workspace(n, dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_experts_nvfp4(_ptr(x), _ptr(top_k_index), _ptr(top_k_weights), _ptr(gate_up), _ptr(gus),
+                                        _ptr(gug), _ptr(down), _ptr(dns), _ptr(dng), S, H, I, E, k, _ptr(out), _ptr(ws),
+                                        ws.numel(), _stream(dev)), "janus_moe_experts_nvfp4")
+    return out
+
+
+@experts_nvfp4.register_fake
+def _(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global):
     return torch.empty_like(x)
 
 

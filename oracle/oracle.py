@@ -3,8 +3,9 @@ cpu_baseline leg of bench.py as the checker; the product (janus_amd) never impor
 
 A numpy restatement of the reference's algorithm on the int4 group-128 codec, with every rounding point explicit:
 
-  dequant   W = RNE_bf16(q * s): the product is exact, one rounding (janus/moe_w4a16.py:9-10 and
-            janus/hybrid.py:417-423 state the same principle for NVFP4).
+  dequant   int4 group-128: W = RNE_bf16(q * s): the product is exact, one rounding.
+            NVFP4 (janus/hybrid.py:400-423, janus/moe_w4a16.py:19-33, 68-72): W = RNE_bf16(RNE_fp32(e2m1 *
+            RNE_fp32(e4m3 * global))), the reference's two fp32 products in its order, then bf16.
   router    logit = RNE_fp32(exact dot product x . w) (+ bias in fp32); the k largest, ties to the lower expert id,
             descending slots; weights = fp32 softmax over all experts, top-k, divided by their sum
             (transformers models/qwen3_5_moe/modeling_qwen3_5_moe.py:770-774).
@@ -64,6 +65,45 @@ def dequant(words, scale_bits) -> np.ndarray:
     q = int4_codes(words).astype(np.float64)
     s = np.repeat(bf16_from_bits(scale_bits), GROUP, axis=-1)
     return bf16_round(q * s)
+
+
+# ---- NVFP4 ------------------------------------------------------------------------------------------------------
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.float64)  # codes 0..7; bit 3 is the sign
+
+
+def e2m1_values(codes) -> np.ndarray:
+    """e2m1 codes (0..15) -> fp64 values (janus/hybrid.py:400-405): bit 3 sign, bits 2-1 exponent, bit 0 mantissa."""
+    c = np.asarray(codes).astype(np.int64)
+    mag = E2M1[c & 7]
+    return np.where(c & 8, -mag, mag)
+
+
+def e4m3_values(bits) -> np.ndarray:
+    """OCP e4m3fn bytes -> fp64 values: sign, 4 exponent bits (bias 7), 3 mantissa bits; exponent 0 is subnormal
+    (m * 2^-9); 0x7F and 0xFF are NaN (the format has no infinities)."""
+    b = np.asarray(bits).astype(np.int64)
+    e, m = (b >> 3) & 15, b & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10))
+    mag = np.where((e == 15) & (m == 7), np.nan, mag)
+    return np.where(b & 0x80, -mag, mag)
+
+
+def f32_round(v) -> np.ndarray:
+    """Nearest-even rounding of fp64 values to fp32, returned as fp64 (numpy's float64 -> float32 cast)."""
+    return np.asarray(v, dtype=np.float64).astype(np.float32).astype(np.float64)
+
+
+def nvfp4_dequant(packed, scale_bits, global_scale) -> np.ndarray:
+    """packed [..., K/2] uint8 (low nibble = even k), e4m3 bytes [..., K/16], fp32 global [...] (one per row) ->
+    W [..., K] as fp64 bf16 values = RNE_bf16(RNE_fp32(e2m1 * RNE_fp32(e4m3 * global))). Each fp64 product is exact
+    (e4m3 * fp32: 4 + 24 bits; e2m1 * fp32: 2 + 24 bits), so the fp32 roundings are the only ones before bf16."""
+    p = np.asarray(packed, dtype=np.uint8)
+    codes = np.stack([p & 15, p >> 4], axis=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
+    g = np.asarray(global_scale, dtype=np.float32).astype(np.float64)
+    S = f32_round(e4m3_values(scale_bits) * g[..., None])            # [..., K/16]
+    v = f32_round(e2m1_values(codes) * np.repeat(S, 16, axis=-1))
+    return bf16_round(v)
 
 
 # ---- router ----------------------------------------------------------------------------------------------------
@@ -171,27 +211,42 @@ def silu(g):
     return g / (1.0 + np.exp(-g))
 
 
-def expert_sum(x, idx, weights, gate_up_q, gate_up_s, down_q, down_s, tokens=None) -> np.ndarray:
-    """Unrounded sum_j w_j * down_e(RNE_bf16(silu(gate_e(x)) * up_e(x))) (fp64) for `tokens` (default all) -> [n, H].
-    x: bf16 values as fp64 [T, H]; idx [T, k]; weights [T, k] (any float dtype, used at its value)."""
+def expert_sum_dq(x, idx, weights, wgu_of, wd_of, tokens=None) -> np.ndarray:
+    """Unrounded sum_j w_j * down_e(RNE_bf16(silu(gate_e(x)) * up_e(x))) (fp64) for `tokens` (default all) -> [n, H],
+    with expert e's dequantised weights wgu_of(e) [2I, H] and wd_of(e) [H, I]. x: bf16 values as fp64 [T, H];
+    idx [T, k]; weights [T, k] (any float dtype, used at its value)."""
     x = np.asarray(x, dtype=np.float64)
     idx = np.asarray(idx, dtype=np.int64)
     weights = np.asarray(weights).astype(np.float64)
     tokens = np.arange(x.shape[0]) if tokens is None else np.asarray(tokens)
     H = x.shape[1]
-    I = np.asarray(gate_up_q).shape[1] // 2
     out = np.zeros((len(tokens), H), dtype=np.float64)
     sel = idx[tokens]                                   # [n, k]
     for e in np.unique(sel):
         rows, slots = np.nonzero(sel == e)
-        wgu = dequant(gate_up_q[e], gate_up_s[e])       # [2I, H]
-        wd = dequant(down_q[e], down_s[e])              # [H, I]
+        wgu = wgu_of(e)
+        wd = wd_of(e)
+        I = wgu.shape[0] // 2
         xe = x[tokens[rows]]
         g, u = xe @ wgu[:I].T, xe @ wgu[I:].T
         h = bf16_round(silu(g) * u)
         y = h @ wd.T
         np.add.at(out, rows, weights[tokens[rows], slots][:, None] * y)
     return out
+
+
+def expert_sum(x, idx, weights, gate_up_q, gate_up_s, down_q, down_s, tokens=None) -> np.ndarray:
+    """expert_sum_dq on int4 group-128 stacks."""
+    return expert_sum_dq(x, idx, weights, lambda e: dequant(gate_up_q[e], gate_up_s[e]),
+                         lambda e: dequant(down_q[e], down_s[e]), tokens)
+
+
+def expert_sum_nvfp4(x, idx, weights, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global,
+                     tokens=None) -> np.ndarray:
+    """expert_sum_dq on NVFP4 stacks: packed [E, N, K/2] uint8, e4m3 bytes [E, N, K/16], global [E, N] fp32."""
+    return expert_sum_dq(x, idx, weights,
+                         lambda e: nvfp4_dequant(gate_up[e], gate_up_scale[e], gate_up_global[e]),
+                         lambda e: nvfp4_dequant(down[e], down_scale[e], down_global[e]), tokens)
 
 
 def shared_sum(x, gate_up_q, gate_up_s, down_q, down_s, gate_w=None, tokens=None) -> np.ndarray:

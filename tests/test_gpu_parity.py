@@ -269,3 +269,96 @@ def test_block_graph_captured_first_in_a_fresh_thread(gpu):
     if "err" in result:
         raise result["err"]
     assert result.get("ok")
+
+
+# ---- NVFP4 (the reference's checkpoint format) -------------------------------------------------------------------
+
+def test_dequant_nvfp4_bit_exact_over_codes_scales_and_globals(gpu):
+    """Every e2m1 code against every finite e4m3 scale byte and globals with full 24-bit significands: the HIP decode
+    equals RNE_bf16(RNE_fp32(e2m1 * RNE_fp32(e4m3 * g))). Also pins the byte order of the fp4 widening."""
+    from janus_amd.hybrid import nvfp4_dequantize
+    sbytes = np.array([b for b in range(256) if (b & 0x7F) != 0x7F], dtype=np.uint8)  # no NaN scales
+    rng = np.random.default_rng(3)
+    globals_ = np.concatenate([[1.0, 2.0 ** -9], rng.uniform(1, 2, 6) * 2.0 ** rng.integers(-14, -2, 6)])
+    globals_ = globals_.astype(np.float32)
+    # one row per (scale byte, global); a row holds two 16-blocks, each with every code once in a different order
+    codes = np.concatenate([np.arange(16), np.arange(16)[::-1]]).astype(np.uint8)
+    row = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8)             # 16 bytes
+    rows = sbytes.size * globals_.size
+    packed = np.broadcast_to(row, (rows, 16)).copy()
+    scale = np.repeat(np.repeat(sbytes, globals_.size)[:, None], 2, axis=1)
+    g = np.tile(globals_, sbytes.size)
+    got = nvfp4_dequantize(torch.from_numpy(packed).to(gpu), torch.from_numpy(scale).view(torch.float8_e4m3fn).to(gpu),
+                           torch.from_numpy(g).to(gpu))
+    got_bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
+    want_bits = O.bf16_to_bits(O.nvfp4_dequant(packed, scale, g))
+    assert np.array_equal(got_bits, want_bits), np.argwhere(got_bits != want_bits)[:5]
+
+
+def _nvfp4_stacks(E, I, H, seed):
+    from janus_amd.hybrid import nvfp4_quantize
+    torch.manual_seed(seed)
+    gu, dn = torch.randn(E, 2 * I, H) * 0.05, torch.randn(E, H, I) * 0.05
+
+    def stack(ts, rows):
+        parts = list(zip(*(nvfp4_quantize(t) for t in ts)))
+        return (torch.stack(parts[0]), torch.stack(parts[1]),
+                torch.stack(parts[2])[:, None, None].expand(E, rows, 1).contiguous())
+
+    return (*stack(gu, 2 * I), *stack(dn, H))
+
+
+def _nvfp4_oracle(x, idx, w, st):
+    gu, gus, gug, dn, dns, dng = (t.cpu() for t in st)
+    E = gu.shape[0]
+    return O.bf16_round(O.expert_sum_nvfp4(bf16_np(x), idx.cpu().numpy(), w.cpu().float().numpy(), gu.numpy(),
+                                           gus.view(torch.uint8).numpy(), gug.reshape(E, -1).numpy(), dn.numpy(),
+                                           dns.view(torch.uint8).numpy(), dng.reshape(E, -1).numpy()))
+
+
+@pytest.mark.parametrize("S", [3, 100, 700])
+def test_fused_moe_nvfp4_reference_test(gpu, S):
+    """tests/test_hybrid.py:725-746 on NVFP4 stacks, the reference's own arguments: E=16, I=512, H=2048, top-8, a hot
+    expert, the last expert never hit, bf16 routing weights. Against the oracle (the layer bar) and against the
+    dequantise path of NVFP4Experts (the reference test's own check)."""
+    from janus_amd.hybrid import NVFP4Experts
+    E, I, H = 16, 512, 2048
+    st = tuple(t.to(gpu) for t in _nvfp4_stacks(E, I, H, seed=0))
+    experts = NVFP4Experts(*st)
+    g = torch.Generator().manual_seed(S)
+    x = (torch.randn(S, H, generator=g) * 0.5).bfloat16().to(gpu)
+    index = torch.randint(0, E - 1, (S, 8), generator=g)
+    index[: S // 2, 0] = 2
+    weights = torch.softmax(torch.randn(S, 8, generator=g), -1).bfloat16()
+    index, weights = index.to(gpu), weights.to(gpu)
+    with torch.no_grad():
+        out = fused_moe(x, index, weights, *st)
+        reference = experts._eager(x, index, weights, experts.gate_up_proj, experts.down_proj)
+    torch.testing.assert_close(out.float(), reference.float(), atol=2e-2, rtol=2e-2)
+    assert (out.float() - reference.float()).abs().max() < 0.02 * reference.float().abs().max() + 1e-3
+    assert_layer_close(bf16_np(out), _nvfp4_oracle(x, index, weights, st), f"nvfp4 S={S}")
+
+
+def test_fused_moe_nvfp4_graph_replay(gpu):
+    """The reference test's graph check: warm-up on a side stream, capture, replay equals the eager result."""
+    E, I, H = 16, 512, 2048
+    st = tuple(t.to(gpu) for t in _nvfp4_stacks(E, I, H, seed=1))
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(64, H, generator=g) * 0.5).bfloat16().to(gpu)
+    index = torch.randint(0, E, (64, 8), generator=g).to(gpu)
+    weights = torch.softmax(torch.randn(64, 8, generator=g), -1).to(gpu)
+    args = (x, index, weights, *st)
+    with torch.no_grad():
+        eager = fused_moe(*args).clone()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            fused_moe(*args)
+        torch.cuda.current_stream().wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            replayed = fused_moe(*args)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(replayed, eager)

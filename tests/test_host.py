@@ -97,6 +97,12 @@ def test_argument_errors_return_codes_without_a_gpu(L):
     assert L.janus_moe_experts(None, p, p, p, p, p, p, 4, 512, 512, 16, 2, p, p, 1 << 30, None) == 1
     assert L.janus_moe_dequant(p, p, 4, 100, p, None) == 1
     assert L.janus_moe_dequant(None, p, 4, 128, p, None) == 1
+    assert L.janus_moe_dequant_nvfp4(p, p, p, 4, 24, p, None) == 1
+    assert L.janus_moe_dequant_nvfp4(p, None, p, 4, 32, p, None) == 1
+    assert L.janus_moe_experts_nvfp4(p, p, p, p, p, p, p, p, p, 4, 200, 512, 16, 2, p, p, 1 << 30, None) == 1
+    assert L.janus_moe_experts_nvfp4(p, p, p, p, p, None, p, p, p, 4, 512, 512, 16, 2, p, p, 1 << 30, None) == 1
+    assert "null" in _err(L)
+    assert L.janus_moe_experts_nvfp4(p, p, p, p, p, p, p, p, p, 4, 512, 512, 16, 2, p, p, 8, None) == 2
     assert L.janus_moe_align(p, 4, 2, 8, 0, p, p, p, p, 1 << 20, None) == 1
     assert L.janus_moe_router_prepare(None, 16, 512, p, 1 << 30, None) == 1
     assert L.janus_moe_block_forward(None, p, 4, p, None, None, p, 1 << 30, None) == 1

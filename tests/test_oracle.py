@@ -343,3 +343,125 @@ def test_block_forward_composes_route_experts_shared_with_one_rounding():
     # sampled tokens give the rows of the full result
     sub, _, _, _ = O.block_forward(L, x, 2, tokens=[1])
     assert np.array_equal(sub[0], out[1])
+
+
+# ---- NVFP4 ------------------------------------------------------------------------------------------------------
+
+def test_e4m3_values_match_torch_on_every_byte():
+    b = np.arange(256)
+    ref = torch.from_numpy(b.astype(np.uint8)).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    got = O.e4m3_values(b)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+
+
+def test_e2m1_values_from_the_bit_fields():
+    """The table against the format's definition: sign bit 3, exponent bits 2-1 (bias 1), mantissa bit 0, exponent 0
+    subnormal (m/2); and the reference's FP4_MAX = 6 (janus/hybrid.py:398)."""
+    for c in range(16):
+        s, e, m = c >> 3, (c >> 1) & 3, c & 1
+        mag = m / 2 if e == 0 else (1 + m / 2) * 2.0 ** (e - 1)
+        want = -mag if s else mag
+        got = O.e2m1_values(np.array([c]))[0]
+        assert got == want and math.copysign(1, got) == math.copysign(1, want), c
+    assert O.e2m1_values(np.arange(16)).max() == 6.0
+
+
+def test_nvfp4_dequant_two_fp32_roundings_then_bf16_exact_rational():
+    """W = RNE_bf16(RNE_fp32(e2m1 * RNE_fp32(e4m3 * g))) against exact rational arithmetic. The sample is searched for
+    elements where each plausible slip changes the result (rounding once from the exact product; dropping the inner
+    or the outer fp32 rounding): all of those, plus random others, are checked exactly."""
+    rng = np.random.default_rng(5)
+    rows = 200_000
+    packed = rng.integers(0, 256, size=(rows, 8), dtype=np.uint8)
+    sbytes = rng.integers(0x08, 0x77, size=(rows, 1)).astype(np.uint8)  # finite, normal-range scales
+    g = (rng.uniform(1.0, 2.0, size=rows) * 2.0 ** rng.integers(-12, -2, size=rows)).astype(np.float32)
+    got = O.nvfp4_dequant(packed, sbytes, g)
+    codes = np.stack([packed & 15, packed >> 4], axis=-1).reshape(rows, 16)
+    v = O.e2m1_values(codes)
+    sc = O.e4m3_values(sbytes)                      # [rows, 1]
+    g64 = g.astype(np.float64)[:, None]
+    slips = {
+        "one rounding from the exact product": O.bf16_round(v * sc * g64),
+        "no inner fp32 rounding": O.bf16_round(O.f32_round(v * (sc * g64))),
+        "no outer fp32 rounding": O.bf16_round(v * O.f32_round(sc * g64)),
+    }
+    picks = set()
+    for name, alt in slips.items():
+        diff = np.argwhere(got != alt)
+        assert len(diff) > 0 or name == "no inner fp32 rounding", name  # the sample exercises this rounding step
+        picks.update(map(tuple, diff[:200]))
+    picks.update(map(tuple, np.stack([rng.integers(0, rows, 300), rng.integers(0, 16, 300)], axis=1)))
+    for i, j in picks:
+        S = round_fraction(Fraction(float(sc[i, 0])) * Fraction(float(g[i])), 24)
+        want = round_fraction(round_fraction(Fraction(float(v[i, j])) * S, 24), 8)
+        assert Fraction(float(got[i, j])) == want, (i, j)
+
+    # The inner rounding shows only where it moves e2m1 * S across a bf16 midpoint: search for such globals with a
+    # full-mantissa scale (e4m3 0x3F = 1.875) and code 5 (3.0), then check those exactly.
+    cand = (rng.uniform(1.0, 2.0, size=4_000_000) * 2.0 ** -6).astype(np.float32).astype(np.float64)
+    inner = O.bf16_round(O.f32_round(3.0 * O.f32_round(1.875 * cand)))
+    hits = cand[inner != O.bf16_round(O.f32_round(3.0 * (1.875 * cand)))][:16]
+    assert len(hits) > 0
+    rows2 = np.full((len(hits), 8), 0x55, dtype=np.uint8)  # code 5 in both nibbles
+    got2 = O.nvfp4_dequant(rows2, np.full((len(hits), 1), 0x3F, dtype=np.uint8), hits.astype(np.float32))
+    for i, gv in enumerate(hits):
+        S = round_fraction(Fraction(15, 8) * Fraction(float(gv)), 24)
+        want = round_fraction(round_fraction(3 * S, 24), 8)
+        assert all(Fraction(float(w)) == want for w in got2[i]), i
+        assert want != round_fraction(round_fraction(3 * Fraction(15, 8) * Fraction(float(gv)), 24), 8)
+
+
+def test_nvfp4_reference_round_trip_and_modules():
+    """tests/test_hybrid.py:545-579 for this module: layout and dtypes, the error bound of quantise -> dequantise,
+    values on the fp4 grid coming back exactly, NVFP4Experts (buffers only, nothing persisted) equal to the dequantised
+    triple loop, NVFP4Linear equal to x W^T; the fp4 activation mode is refused."""
+    from janus_amd.hybrid import NVFP4Experts, NVFP4Linear, _e2m1_decode, nvfp4_dequantize, nvfp4_quantize
+    torch.manual_seed(0)
+    w = torch.randn(48, 64) * 3
+    packed, scale, g = nvfp4_quantize(w)
+    assert packed.dtype == torch.uint8 and packed.shape == (48, 32) and scale.dtype == torch.float8_e4m3fn
+    assert scale.shape == (48, 4) and g.shape == ()
+    amax = w.view(48, 4, 16).abs().amax(-1).repeat_interleave(16, -1)
+    assert ((nvfp4_dequantize(packed, scale, g, torch.float32) - w).abs() <= amax / 6 * (1 + 1 / 16) + 1e-6).all()
+    codes = torch.randint(0, 16, (48, 64), dtype=torch.uint8)
+    codes[:, ::16] = 7  # every block carries a +6, so the block scale is re-derived exactly
+    grid = _e2m1_decode(codes) * scale.float().repeat_interleave(16, -1) * g
+    torch.testing.assert_close(nvfp4_dequantize(*nvfp4_quantize(grid, g), torch.float32), grid, atol=1e-6, rtol=1e-6)
+    E, I, H = 8, 32, 64
+    gu, dn = torch.randn(E, 2 * I, H), torch.randn(E, H, I)
+
+    def stack(ts, rows):
+        parts = list(zip(*(nvfp4_quantize(t) for t in ts)))
+        return (torch.stack(parts[0]), torch.stack(parts[1]),
+                torch.stack(parts[2])[:, None, None].expand(E, rows, 1).contiguous())
+
+    experts = NVFP4Experts(*stack(gu, 2 * I), *stack(dn, H))
+    assert not any(True for _ in experts.parameters()) and not experts.state_dict()
+    x, index, weights = torch.randn(10, H), torch.randint(0, E, (10, 2)), torch.rand(10, 2)
+    out = experts(x, index, weights)
+    GU, DN = experts.gate_up_proj.float(), experts.down_proj.float()
+    ref = torch.zeros_like(x)
+    for t in range(10):
+        for k in range(2):
+            gate, up = (x[t] @ GU[index[t, k]].T).chunk(2)
+            ref[t] += weights[t, k] * (torch.nn.functional.silu(gate) * up) @ DN[index[t, k]].T
+    torch.testing.assert_close(out, ref, atol=1e-3, rtol=1e-3)
+    linear = NVFP4Linear(*nvfp4_quantize(torch.randn(32, 64)))
+    torch.testing.assert_close(linear(x), x @ linear.weight.float().T, atol=1e-3, rtol=1e-3)
+    with pytest.raises(ValueError):
+        linear.set_mode(fp4=True)
+
+
+def test_nvfp4_cpu_dequantize_matches_oracle_bit_for_bit():
+    """The module's CPU decode (torch, janus_amd.hybrid) against the oracle on every code and a sweep of scale bytes
+    and globals."""
+    from janus_amd.hybrid import nvfp4_dequantize
+    rng = np.random.default_rng(9)
+    rows = 64
+    packed = rng.integers(0, 256, size=(rows, 64), dtype=np.uint8)
+    sbytes = rng.integers(0, 0x7F, size=(rows, 8)).astype(np.uint8)
+    g = (rng.uniform(0.5, 2.0, size=rows) * 2.0 ** -8).astype(np.float32)
+    got = nvfp4_dequantize(torch.from_numpy(packed), torch.from_numpy(sbytes).view(torch.float8_e4m3fn),
+                           torch.from_numpy(g)[:, None])
+    assert np.array_equal(O.bf16_values(got), O.nvfp4_dequant(packed, sbytes, g))
