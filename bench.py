@@ -7,9 +7,11 @@ gated shared expert, combine) through the HIP path.
 Timed region: W untimed forwards, then K forwards launched back to back on one stream, bracketed by device
 synchronisation. Inputs and weights are resident in HBM before it starts. In every timed step the library records
 HIP events on its launch stream at the stage boundaries (janus_moe_profile_events), each step into its own events,
-so the per-kernel averages cover exactly the timed steps. The dominant kernel (the gate_up GEMM) gives the roofline
-entry; its HBM traffic per launch comes from two rocprofv3 --pmc child runs of this script (FETCH_SIZE, then
-WRITE_SIZE), each scaled by what the same counter reads for a device copy of known size. The same layer replayed
+so the per-kernel averages cover exactly the timed steps. The dominant kernel (both grouped GEMMs, gate_up and down,
+in one persistent launch) gives the roofline entry; its HBM traffic per launch comes from two rocprofv3 --pmc child
+runs of this script (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same counter reads for a device copy of
+known size. With JANUS_MOE_SCHEDULE=split in the environment the GEMMs run as one launch each (the A/B reference):
+the stages then also report gate_up and down, and the traffic entry is null. The same layer replayed
 from a HIP graph is timed afterwards and reported as graph_tokens_per_s. The CPU baseline is the reference's CPU
 algorithm (dequantise-per-call + padded bmm, oracle/cpu_bmm.py) on the same inputs, on all host cores, on a bounded
 sample. Prints one JSON line.
@@ -35,14 +37,15 @@ import torch
 METRIC = "MoE layer tokens/s at T=2048 (35B-A3B shape); % of HBM/MFMA roofline"
 HBM_PEAK = 8.0e12        # bytes/s, MI355X
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 FLOP/s, MI355X
-STAGES = ("route", "align", "gate_up", "down", "combine")
-GATE_UP_KERNEL = r"w4a16_\w+_kernel<0,"     # the gate_up instantiations (pipelined or generic)
+STAGES = ("route", "align", "gate_up", "down", "combine")  # the library's event boundaries
+EXPERTS_KERNEL = r"moe_experts_kernel<"      # gate_up + down in one persistent launch
 COPY_MIB = 256
 HERE = Path(__file__).resolve().parent
 
 
 def layer_work(cfg, idx: np.ndarray) -> dict:
-    """Algorithmic work of one layer forward and of its gate_up launch, from the realised routing."""
+    """Algorithmic work of one layer forward and of its expert GEMMs (gate_up + down, routed + shared), from the
+    realised routing. The intermediate h is not algorithmic; the GEMMs' algorithmic output is the [T, H] bf16 sum."""
     T, H, E, k, I, I_s = cfg.T, cfg.H, cfg.E, cfg.k, cfg.I, cfg.I_s
     n_hit = int(np.count_nonzero(np.bincount(idx.reshape(-1), minlength=E)))
     A = T * k
@@ -52,9 +55,9 @@ def layer_work(cfg, idx: np.ndarray) -> dict:
     b_sdn = H * I_s // 2 + H * (I_s // 128) * 2
     flops = T * (2 * E * H + 6 * k * I * H + 6 * I_s * H + 2 * H)
     layer_bytes = n_hit * (b_gu + b_dn) + b_sgu + b_sdn + (H * 2 if I_s else 0) + E * H * 4 + 2 * T * H * 2
-    gu_bytes = n_hit * b_gu + b_sgu + T * H * 2 + (A * I + T * I_s) * 2   # weights, x read, h written
-    gu_flops = 2 * A * H * 2 * I + 2 * T * H * 2 * I_s
-    return dict(n_hit=n_hit, flops=flops, bytes=layer_bytes, gu_bytes=gu_bytes, gu_flops=gu_flops)
+    ex_bytes = n_hit * (b_gu + b_dn) + b_sgu + b_sdn + 2 * T * H * 2            # weights, x read, output written
+    ex_flops = 6 * A * I * H + 6 * T * I_s * H
+    return dict(n_hit=n_hit, flops=flops, bytes=layer_bytes, ex_bytes=ex_bytes, ex_flops=ex_flops)
 
 
 def cpu_baseline(layer, x, k, budget_s: float = 30.0) -> dict:
@@ -136,14 +139,14 @@ def _profile(counter: str, child_args: list[str], kernel_substr: str, timeout: i
 
 
 def pmc_traffic(config: str) -> dict:
-    """HBM bytes per gate_up launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by the ratio of
+    """HBM bytes per experts launch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by the ratio of
     the known bytes of a COPY_MIB MiB device copy to what the same counter reads for it."""
     copy_bytes = COPY_MIB << 20
     fetch_copy = _profile("FETCH_SIZE", ["--copy-calibration", str(COPY_MIB)], "copyBuffer")
     write_copy = _profile("WRITE_SIZE", ["--copy-calibration", str(COPY_MIB)], "copyBuffer")
     f_fetch, f_write = copy_bytes / (fetch_copy * 1024), copy_bytes / (write_copy * 1024)
-    fetch = _profile("FETCH_SIZE", ["--config", config], GATE_UP_KERNEL) * 1024 * f_fetch
-    write = _profile("WRITE_SIZE", ["--config", config], GATE_UP_KERNEL) * 1024 * f_write
+    fetch = _profile("FETCH_SIZE", ["--config", config], EXPERTS_KERNEL) * 1024 * f_fetch
+    write = _profile("WRITE_SIZE", ["--config", config], EXPERTS_KERNEL) * 1024 * f_write
     return {"fetch_bytes": fetch, "write_bytes": write, "fetch_scale": f_fetch, "write_scale": f_write}
 
 
@@ -203,7 +206,12 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     ms = elapsed / args.steps * 1e3
     stage_ms = np.array([[row[j].elapsed_time(row[j + 1]) for j in range(len(STAGES))] for row in events])
-    stage_us = {n: float(v) * 1e3 for n, v in zip(STAGES, stage_ms.mean(0))}
+    raw_us = {n: float(v) * 1e3 for n, v in zip(STAGES, stage_ms.mean(0))}
+    split = os.environ.get("JANUS_MOE_SCHEDULE") == "split"
+    stage_us = {"route": raw_us["route"], "align": raw_us["align"], "experts": raw_us["gate_up"] + raw_us["down"],
+                "combine": raw_us["combine"]}
+    if split:
+        stage_us.update(gate_up=raw_us["gate_up"], down=raw_us["down"])
 
     # the same forward replayed from a HIP graph (the reference serves under graphs)
     side = torch.cuda.Stream(device=dev)
@@ -223,18 +231,20 @@ def main() -> int:
     torch.cuda.synchronize()
     graph_s = (time.perf_counter() - t1) / args.steps
 
-    gu_s = stage_us["gate_up"] * 1e-6
+    ex_s = stage_us["experts"] * 1e-6
     t_step = ms * 1e-3
     t_roof = max(work["flops"] / MFMA_BF16_PEAK, work["bytes"] / HBM_PEAK)
-    if work["gu_bytes"] / HBM_PEAK >= work["gu_flops"] / MFMA_BF16_PEAK:
-        ach = work["gu_bytes"] / gu_s / 1e9
+    if work["ex_bytes"] / HBM_PEAK >= work["ex_flops"] / MFMA_BF16_PEAK:
+        ach = work["ex_bytes"] / ex_s / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": ach / (HBM_PEAK / 1e9)}
     else:
-        ach = work["gu_flops"] / gu_s / 1e12
+        ach = work["ex_flops"] / ex_s / 1e12
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                 "frac": ach / (MFMA_BF16_PEAK / 1e12)}
     traffic, traffic_note = None, "skipped (--no-pmc)"
-    if not args.no_pmc:
+    if split:
+        traffic_note = "skipped: JANUS_MOE_SCHEDULE=split runs the GEMMs as two launches"
+    elif not args.no_pmc:
         try:
             t = pmc_traffic(args.config)
             traffic = t["fetch_bytes"] + t["write_bytes"]
@@ -243,8 +253,9 @@ def main() -> int:
                             f"write {t['write_bytes']:.4g} B per launch")
         except Exception as exc:  # no profiler on this machine: the entry stays null, with the reason
             traffic_note = f"unavailable: {type(exc).__name__}: {exc}"[:300]
-    roof.update({"traffic": traffic, "kernel": "w4a16_gemm_kernel<gate_up>", "algorithmic_bytes": work["gu_bytes"],
-                 "algorithmic_flops": work["gu_flops"], "avg_us": stage_us["gate_up"], "traffic_source": traffic_note})
+    kernel = "w4a16_gemm_kernel<gate_up> + <down> (split)" if split else "moe_experts_kernel (gate_up + down)"
+    roof.update({"traffic": traffic, "kernel": kernel, "algorithmic_bytes": work["ex_bytes"],
+                 "algorithmic_flops": work["ex_flops"], "avg_us": stage_us["experts"], "traffic_source": traffic_note})
 
     result = {
         "metric": METRIC, "value": cfg.T / t_step, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,

@@ -29,6 +29,9 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     # packed fp32 VALU ops stay off: plain fp32 code only
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # atomics stay one instruction per wave: the optimizer's broadcast of a returned value waits for the atomic where
+    # it is issued, and the persistent GEMM launch takes its next ticket early so that the wait falls a unit later
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]

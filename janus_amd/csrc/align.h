@@ -18,10 +18,11 @@ struct AlignWorkspace {
 AlignWorkspace carve_align(Carver& c, int A, int E);
 
 // sorted_ids [sorted_len] gets the permutation, the sentinel A everywhere else. Either expert_ids/total (reference tile
-// plan, `tiles` entries) or chunks/num_chunks (runs of at most chunk_rows rows of one expert) may be null.
+// plan, `tiles` entries) or chunks/num_chunks (runs of at most chunk_rows rows of one expert) may be null. clear[0 ..
+// clear_n) is set to zero on the side (the counters of a later launch; null when clear_n == 0).
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
-                 OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
-                 hipStream_t stream);
+                 OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks, int* clear,
+                 int clear_n, hipStream_t stream);
 
 }  // namespace janus

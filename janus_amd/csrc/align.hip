@@ -69,8 +69,10 @@ __device__ __forceinline__ Peers wave_peers(int e, int nbits) {
 // holds expert tid's count and start. Called by every thread of the workgroup.
 template <typename OutT>
 __device__ void write_plan(const int* cum, int E, int block, int count, int start, OutT* expert_ids, int tiles,
-                           OutT* total_out, int4* chunks, int chunk_rows, int* num_chunks, int* scan_tmp) {
+                           OutT* total_out, int4* chunks, int chunk_rows, int* num_chunks, int* scan_tmp,
+                           int* clear, int clear_n) {
   const int tid = threadIdx.x, nthreads = blockDim.x;
+  for (int i = tid; i < clear_n; i += nthreads) clear[i] = 0;
   if (expert_ids) {
     for (int i = tid; i < tiles; i += nthreads) {
       const long key = (long)i * block;
@@ -144,7 +146,8 @@ template <typename IdxT, typename OutT>
 __global__ void __launch_bounds__(kPlaceThreads) align_small_place_kernel(
     const IdxT* __restrict__ idx, int A, int E, int block, int nb, const int* __restrict__ hist,
     const int* __restrict__ local_rank, OutT* __restrict__ sorted_ids, int sorted_len, OutT* __restrict__ expert_ids,
-    int tiles, OutT* __restrict__ total_out, int4* __restrict__ chunks, int chunk_rows, int* __restrict__ num_chunks) {
+    int tiles, OutT* __restrict__ total_out, int4* __restrict__ chunks, int chunk_rows, int* __restrict__ num_chunks,
+    int* __restrict__ clear, int clear_n) {
   __shared__ int cum[kMaxExperts];
   __shared__ int base[kMaxExperts];
   __shared__ int part_count[kPlaceThreads], part_before[kPlaceThreads];
@@ -201,7 +204,7 @@ __global__ void __launch_bounds__(kPlaceThreads) align_small_place_kernel(
     const int total = E > 0 ? cum[E - 1] : 0;
     for (int i = total + tid; i < sorted_len; i += kPlaceThreads) sorted_ids[i] = (OutT)A;
     write_plan<OutT>(cum, E, block, count, start, expert_ids, tiles, total_out, chunks, chunk_rows, num_chunks,
-                     scan_tmp);
+                     scan_tmp, clear, clear_n);
   }
 }
 
@@ -253,7 +256,8 @@ __global__ void __launch_bounds__(kScanThreads) align_scan_kernel(int* __restric
                                                                   int* __restrict__ counts, int* __restrict__ start,
                                                                   OutT* __restrict__ expert_ids, int tiles,
                                                                   OutT* __restrict__ total_out, int4* __restrict__ chunks,
-                                                                  int chunk_rows, int* __restrict__ num_chunks) {
+                                                                  int chunk_rows, int* __restrict__ num_chunks,
+                                                                  int* __restrict__ clear, int clear_n) {
   __shared__ int cum[kMaxExperts];
   __shared__ int waves[16];
   const int tid = threadIdx.x;
@@ -274,7 +278,7 @@ __global__ void __launch_bounds__(kScanThreads) align_scan_kernel(int* __restric
   }
   __syncthreads();
   write_plan<OutT>(cum, E, block, c, tid < E ? start[tid] : 0, expert_ids, tiles, total_out, chunks, chunk_rows,
-                   num_chunks, waves);
+                   num_chunks, waves, clear, clear_n);
 }
 
 template <typename IdxT, typename OutT>
@@ -315,7 +319,7 @@ AlignWorkspace carve_align(Carver& c, int A, int E) {
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
-                 hipStream_t stream) {
+                 int* clear, int clear_n, hipStream_t stream) {
   if (A <= kSmallMaxA) {
     const int nb = ceil_div(A, kSmallBlock);
     if (nb > 0) {
@@ -325,7 +329,7 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
     }
     hipLaunchKernelGGL((align_small_place_kernel<IdxT, OutT>), dim3(nb > 0 ? nb : 1), dim3(kPlaceThreads), 0, stream,
                        idx, A, E, block, nb, w.hist, w.local_rank, sorted_ids, sorted_len, expert_ids, tiles, total,
-                       chunks, chunk_rows, num_chunks);
+                       chunks, chunk_rows, num_chunks, clear, clear_n);
     JANUS_LAUNCH_CHECK("align_small_place");
     return JANUS_MOE_OK;
   }
@@ -337,7 +341,7 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
                      expert_bits(E), w.hist, w.local_rank, sorted_ids, sorted_len);
   JANUS_LAUNCH_CHECK("align_rank");
   hipLaunchKernelGGL((align_scan_kernel<OutT>), dim3(1), dim3(kScanThreads), 0, stream, w.hist, nb, E, block, w.counts,
-                     w.start, expert_ids, tiles, total, chunks, chunk_rows, num_chunks);
+                     w.start, expert_ids, tiles, total, chunks, chunk_rows, num_chunks, clear, clear_n);
   JANUS_LAUNCH_CHECK("align_scan");
   hipLaunchKernelGGL((align_scatter_kernel<IdxT, OutT>), dim3(nb), dim3(kRankThreads), 0, stream, idx, A, E, w.hist,
                      w.local_rank, w.start, sorted_ids);
@@ -346,11 +350,11 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
 }
 
 template int launch_align<int64_t, int64_t>(const int64_t*, int, int, int, const AlignWorkspace&, int64_t*, int,
-                                            int64_t*, int, int64_t*, int4*, int, int*, hipStream_t);
+                                            int64_t*, int, int64_t*, int4*, int, int*, int*, int, hipStream_t);
 template int launch_align<int64_t, int>(const int64_t*, int, int, int, const AlignWorkspace&, int*, int, int*, int,
-                                        int*, int4*, int, int*, hipStream_t);
+                                        int*, int4*, int, int*, int*, int, hipStream_t);
 template int launch_align<int, int>(const int*, int, int, int, const AlignWorkspace&, int*, int, int*, int, int*,
-                                    int4*, int, int*, hipStream_t);
+                                    int4*, int, int*, int*, int, hipStream_t);
 
 }  // namespace janus
 
@@ -379,5 +383,5 @@ extern "C" int janus_moe_align(const int64_t* top_k_index, int S, int top_k, int
   AlignWorkspace w = carve_align(c, (int)A, E);
   const long tiles = (A + (long)E * (block - 1) + block - 1) / block;
   return launch_align<int64_t, int64_t>(top_k_index, (int)A, E, block, w, sorted_ids, (int)(tiles * block), expert_ids,
-                                        (int)tiles, total, nullptr, 0, nullptr, (hipStream_t)stream);
+                                        (int)tiles, total, nullptr, 0, nullptr, nullptr, 0, (hipStream_t)stream);
 }

@@ -43,7 +43,8 @@ struct ExpertsWorkspace {
   uint16_t* h;      // [P, I]
   uint16_t* h_sh;   // [T, I_s]
   float* slots;     // [T, nslots, H] weighted expert outputs
-  int P, C, nslots;
+  int* sched;       // [nsched] counters of the persistent GEMM launch, cleared by align
+  int P, C, nslots, nsched;
 };
 
 ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I, int I_s) {
@@ -55,6 +56,8 @@ ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I,
   w.sorted_ids = c.take<int>(w.P);
   w.chunks = c.take<int4>(w.C);
   w.num_chunks = c.take<int>(1);
+  w.nsched = sched_words(w.C, I_s > 0 ? ceil_div(T, kChunkRows) : 0);
+  w.sched = c.take<int>(w.nsched);
   w.h = c.take<uint16_t>((size_t)w.P * I);
   w.h_sh = c.take<uint16_t>((size_t)T * I_s);
   w.nslots = top_k + (I_s > 0 ? 1 : 0);
@@ -81,7 +84,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   const int A = T * top_k;
   mark(1, stream);
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
-                                   kChunkRows, w.num_chunks, stream);
+                                   kChunkRows, w.num_chunks, w.sched, w.nsched, stream);
   if (rc) return rc;
   const bool shared = I_s > 0;
   GemmParams p = {};
@@ -108,28 +111,34 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.nslab = ceil_div(I > I_s ? I : I_s, 128);
   p.h = w.h;
   p.h_sh = w.h_sh;
-  mark(2, stream);
-  rc = launch_gate_up(p, stream);
-  if (rc) return rc;
   // down: weighted expert outputs into the slots
-  p.a = w.h;
-  p.a_sh = w.h_sh;
-  p.q = dq;
-  p.s = ds;
-  p.gsc = dn_global;
-  p.N = H;
-  p.K = I;
-  p.q_sh = sdq;
-  p.s_sh = sds;
-  p.N_sh = H;
-  p.K_sh = I_s;
-  p.nslab = ceil_div(H, 256);
-  p.slots = w.slots;
-  p.nslots = w.nslots;
-  p.route_w = route_w;
-  p.gamma = gamma;
-  mark(3, stream);
-  rc = launch_down(p, stream);
+  GemmParams d = p;
+  d.a = w.h;
+  d.a_sh = w.h_sh;
+  d.q = dq;
+  d.s = ds;
+  d.gsc = dn_global;
+  d.N = H;
+  d.K = I;
+  d.q_sh = sdq;
+  d.s_sh = sds;
+  d.N_sh = H;
+  d.K_sh = I_s;
+  d.nslab = ceil_div(H, 256);
+  d.slots = w.slots;
+  d.nslots = w.nslots;
+  d.route_w = route_w;
+  d.gamma = gamma;
+  mark(2, stream);
+  rc = launch_experts_fused(p, d, w.sched, stream);  // both GEMMs, one persistent launch
+  if (rc == kNotFused) {
+    rc = launch_gate_up(p, stream);
+    if (rc) return rc;
+    mark(3, stream);
+    rc = launch_down(d, stream);
+  } else {
+    mark(3, stream);
+  }
   if (rc) return rc;
   mark(4, stream);
   rc = launch_combine(w.slots, w.nslots, out, T, H, stream);

@@ -41,6 +41,16 @@ struct GemmParams {
   const float* gamma;         // down: shared-expert weight per token [T], null = 1
 };
 
+// Scheduler words of the persistent launch, zero before it (the align launch clears them): 8 ticket counters, an
+// error word, then one done counter per chunk.
+constexpr int kSchedWordsFixed = 16;
+__host__ __device__ inline int sched_words(int max_chunks, int n_shared_chunks) {
+  return kSchedWordsFixed + max_chunks + n_shared_chunks;
+}
+constexpr int kNotFused = 1;  // launch_experts_fused: no persistent kernel for these sizes (or JANUS_MOE_SCHEDULE=split)
+
+// gate_up then down in one persistent launch (sched: sched_words() ints, zero); kNotFused when it does not apply.
+int launch_experts_fused(const GemmParams& gu, const GemmParams& dn, int* sched, hipStream_t stream);
 int launch_gate_up(const GemmParams& p, hipStream_t stream);
 int launch_down(const GemmParams& p, hipStream_t stream);
 // out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32.

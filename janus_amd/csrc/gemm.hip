@@ -14,6 +14,8 @@
 // lane's accumulator holds 4 consecutive output columns of one row. Workgroup ids are dealt to the 8 XCDs round-robin;
 // the slabs of one chunk get ids that land on the same XCD, so the chunk's activation rows come from that XCD's L2
 // after the first slab.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "gemm.h"
@@ -167,21 +169,23 @@ struct Codec<kNvfp4> {
 
 // NKB: k stages (K / 128) fixed at compile time, the whole k loop unrolled so the compiler's wait counts for the
 // weight registers are exact (a runtime loop makes it wait for every outstanding load); 0 = runtime K.
+//
+// One work unit: chunk c (c < n_shared_chunks: shared-expert tokens c * kChunkRows.., else routed chunk
+// c - n_shared_chunks) times column slab `slab`. lds: the workgroup's LDS double buffer of activation tiles,
+// [buffer][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16 lanes of a fragment read (same chunk, 16
+// rows) hit 16 different bank groups. Uniform over the workgroup; a unit past the chunk list or the columns does
+// nothing.
 template <int MODE, int NKB, int CODEC>
-__global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
+__device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams& p, int c, int slab,
+                                                                unsigned char* lds) {
   using C = Codec<CODEC>;
-  // LDS double buffer of activation tiles, [buffer][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16
-  // lanes of a fragment read (same chunk, 16 rows) hit 16 different bank groups.
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
-
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  int tid = threadIdx.x;
+  // the lane's index math is redone for every unit: kept from a caller's earlier iteration, it would hold registers
+  // across the whole k loop
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
   const int g = lane >> 4, nl = lane & 15;
 
-  // ---- work item: chunk c, column slab ----
-  const int xcd = blockIdx.x & 7, within = blockIdx.x >> 3;
-  const int c = (within / p.nslab) * 8 + xcd;
-  const int slab = within % p.nslab;
-  if (c >= p.n_shared_chunks + p.max_chunks) return;
   const bool shared = c < p.n_shared_chunks;
   int pos0, rows, N, K;
   const int32_t* wq;
@@ -372,6 +376,93 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
   }
 }
 
+// One launch per GEMM: workgroup ids are dealt to the 8 XCDs round-robin, and the slabs of chunk c go to ids on XCD
+// c mod 8, so they share its L2.
+template <int MODE, int NKB, int CODEC>
+__global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
+  const int xcd = blockIdx.x & 7, within = blockIdx.x >> 3;
+  const int c = (within / p.nslab) * 8 + xcd;
+  if (c >= p.n_shared_chunks + p.max_chunks) return;
+  gemm_unit<MODE, NKB, CODEC>(p, c, within % p.nslab, lds);
+}
+
+// Both GEMMs in one persistent launch of two workgroups per CU. The work units sit in one queue per XCD: queue q holds
+// the chunks c = q, q + nq, ... (shared-expert chunks first, as c counts them first), their gate_up units chunk by
+// chunk, then their down units in the same order. A workgroup reads the id of the XCD it runs on and takes tickets from
+// that queue until it runs dry, so every unit of a chunk, producer or consumer of its h rows, runs under one L2, and
+// the down units of early chunks fill the CUs that gate_up's last units leave idle.
+// A down unit waits until all gate_up units of its chunk have counted themselves done. It never waits for a unit
+// without a workgroup: each gate_up unit it depends on has a lower ticket of the same queue, so a running workgroup
+// took it, and gate_up units wait for nothing. The wait is bounded: past spin_limit polls it sets the error word and
+// goes on (the results are then wrong; the launch still ends).
+constexpr int kSchedQueues = 8;   // ticket counters, one per XCD
+constexpr int kSchedError = 8;    // set when a wait gave up
+constexpr int kXccIdReg = 20 | (0 << 6) | ((16 - 1) << 11);  // s_getreg operand: HW_REG_XCC_ID, bits 0..15
+
+template <int NKB_GU, int NKB_DN, int CODEC>
+__global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmParams gu, const GemmParams dn,
+                                                                  int* __restrict__ sched, int nq, int spin_limit) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
+  __shared__ int ticket;
+  // Every branch of this loop is uniform over a wave: wave 0 does the bookkeeping with all its lanes. A branch on the
+  // thread id would give the loop a per-lane exit, and the compiler may then run the other lanes around the loop ahead
+  // of lane 0, through barriers, on a stale ticket. The counters are bumped by buffer atomics that only lane 0 keeps
+  // in range: the hardware drops the other lanes' out-of-range atomics (same-address atomics from 64 lanes would run
+  // one after another).
+  const bool first_wave = __builtin_amdgcn_readfirstlane(threadIdx.x) < kWave;
+  const int nwords = sched_words(gu.max_chunks, gu.n_shared_chunks);
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(sched, (short)0, nwords * 4, 0x00020000);
+  const bool lane0 = (threadIdx.x & (kWave - 1)) == 0;
+  auto bump = [&](int word) __attribute__((always_inline)) {  // sched[word] += 1 by lane 0; the old value in lane 0
+    return __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, srsrc, lane0 ? word * 4 : 0x7FFFFFF0, 0, 0);
+  };
+  const int q = (int)(__builtin_amdgcn_s_getreg(kXccIdReg) & 0xF) % nq;
+  const int* done = sched + kSchedWordsFixed;  // per chunk c
+  const int total = gu.n_shared_chunks + *gu.num_chunks;
+  const int ncq = total > q ? (total - q + nq - 1) / nq : 0;
+  const int ngu = ncq * gu.nslab, nall = ngu + ncq * dn.nslab;
+  if (first_wave) ticket = __builtin_amdgcn_readfirstlane(bump(q));
+  __syncthreads();
+  int t = __builtin_amdgcn_readfirstlane(ticket);
+  while (t < nall) {
+    // the next ticket's atomic (a few microseconds when the GEMMs load the memory system) is in flight during this
+    // unit. Holding two tickets cannot deadlock either: a workgroup whose next ticket is a gate_up unit holds a gate_up
+    // unit now (the queue lists every gate_up unit before the first down unit), and gate_up units wait for nothing.
+    int next = 0;
+    if (first_wave) next = bump(q);
+    if (t < ngu) {
+      const int c = __builtin_amdgcn_readfirstlane(q + nq * (t / gu.nslab));
+      gemm_unit<kGateUp, NKB_GU, CODEC>(gu, c, t % gu.nslab, lds);
+      // every wave's h stores have reached the L2 before the count that publishes them
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (first_wave) (void)bump(kSchedWordsFixed + c);
+    } else {
+      const int u = t - ngu;
+      const int c = __builtin_amdgcn_readfirstlane(q + nq * (u / dn.nslab));
+      if (first_wave) {
+        for (int spins = 0;; ++spins) {
+          const int n = __builtin_amdgcn_readfirstlane(
+              __hip_atomic_load(done + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          if (n >= gu.nslab) break;
+          if (spins >= spin_limit) {
+            __hip_atomic_store(sched + kSchedError, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+        asm volatile("buffer_inv sc0" ::: "memory");  // this CU's L1 drops any stale copy of the chunk's h rows
+      }
+      __syncthreads();
+      gemm_unit<kDown, NKB_DN, CODEC>(dn, c, u % dn.nslab, lds);
+    }
+    if (first_wave) ticket = __builtin_amdgcn_readfirstlane(next);
+    __syncthreads();
+    t = __builtin_amdgcn_readfirstlane(ticket);
+  }
+}
+
 // out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order. The loads of up to 8 slots
 // are issued together before the additions.
 __global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4) {
@@ -467,7 +558,51 @@ int launch_gemm(const GemmParams& params, hipStream_t stream) {
   return JANUS_MOE_OK;
 }
 
+struct DeviceShape {
+  int cus, xccs;
+};
+DeviceShape device_shape() {
+  static DeviceShape cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceShape{0, 0};
+  DeviceShape& d = cache[dev];
+  if (d.cus == 0) {
+    int cus = 0, xccs = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+    if (hipDeviceGetAttribute(&xccs, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) xccs = 0;
+    d.xccs = xccs;
+    d.cus = cus;
+  }
+  return d;
+}
+
 }  // namespace
+
+int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* sched, hipStream_t stream) {
+  const char* env = getenv("JANUS_MOE_SCHEDULE");
+  if (env && strcmp(env, "split") == 0) return kNotFused;
+  GemmParams gu = gu_in, dn = dn_in;
+  if (gu.n_shared_chunks + gu.max_chunks == 0) return kNotFused;
+  if (gu.n_shared_chunks && (gu.K_sh != gu.K || dn.K_sh != dn.K)) return kNotFused;
+  const DeviceShape d = device_shape();
+  if (d.cus <= 0 || d.xccs <= 0) return kNotFused;
+  const int nq = d.xccs < kSchedQueues ? d.xccs : kSchedQueues;
+  gu.nslab = ceil_div(max(gu.N, gu.N_sh) / 2, slab_cols<kGateUp>());
+  dn.nslab = ceil_div(max(dn.N, dn.N_sh), slab_cols<kDown>());
+  const int nkb_gu = gu.K / KS, nkb_dn = dn.K / KS;
+  const dim3 g((unsigned)(2 * d.cus)), b(kThreads);
+  constexpr int kSpinLimit = 1 << 18;  // polls of about 1 us: a wait lasts at most one gate_up unit
+  if (gu.codec == kInt4 && nkb_gu == 16 && nkb_dn == 4)
+    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kInt4>), g, b, 0, stream, gu, dn, sched, nq, kSpinLimit);
+  else if (gu.codec == kInt4 && nkb_gu == 4 && nkb_dn == 2)
+    hipLaunchKernelGGL((moe_experts_kernel<4, 2, kInt4>), g, b, 0, stream, gu, dn, sched, nq, kSpinLimit);
+  else if (gu.codec == kNvfp4 && gu.gsc && dn.gsc && nkb_gu == 16 && nkb_dn == 4)
+    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kNvfp4>), g, b, 0, stream, gu, dn, sched, nq, kSpinLimit);
+  else
+    return kNotFused;
+  JANUS_LAUNCH_CHECK("w4a16 experts");
+  return JANUS_MOE_OK;
+}
 
 int launch_gate_up(const GemmParams& p, hipStream_t stream) { return launch_gemm<kGateUp>(p, stream); }
 int launch_down(const GemmParams& p, hipStream_t stream) { return launch_gemm<kDown>(p, stream); }

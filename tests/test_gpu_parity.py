@@ -244,6 +244,50 @@ def test_block_graph_replay_matches_eager(gpu):
     _replays_match_eager(blk, x)
 
 
+@pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf"])
+def test_persistent_schedule_equals_one_launch_per_gemm(gpu, name, monkeypatch):
+    """Both GEMMs in one persistent launch (a ticket queue per XCD, down units waiting for their chunk's gate_up
+    units) against one launch per GEMM: the same units in another order, so the same bits. The calls in a row reuse
+    the scheduler counters the align launch clears."""
+    cfg = synth.CONFIGS[name]
+    _, blk = _block(cfg, gpu)
+    x = synth.activations(cfg).to(gpu)
+    with torch.no_grad():
+        monkeypatch.setenv("JANUS_MOE_SCHEDULE", "split")
+        split = blk(x).clone()
+        monkeypatch.delenv("JANUS_MOE_SCHEDULE")
+        for _ in range(3):
+            out = blk(x)
+            torch.cuda.synchronize()
+            assert torch.equal(out, split)
+
+
+@pytest.mark.parametrize("S", [1, 3, 700])
+def test_persistent_schedule_fused_moe_int4_and_nvfp4(gpu, S, monkeypatch):
+    """fused_moe on both codecs, one token (most XCD queues empty) to several chunks per expert: the persistent launch
+    equals one launch per GEMM bit for bit."""
+    E, I, H = 16, 512, 2048
+    st = tuple(t.to(gpu) for t in _nvfp4_stacks(E, I, H, seed=2))
+    cfg = synth.LayerConfig("case", T=S, H=H, E=E, k=8, I=I)
+    L = synth.layer(cfg, 3)
+    gq, gs, dq, ds = (L[n].to(gpu) for n in ("gate_up_q", "gate_up_s", "down_q", "down_s"))
+    g = torch.Generator().manual_seed(S)
+    x = (torch.randn(S, H, generator=g) * 0.5).bfloat16().to(gpu)
+    index = torch.randint(0, E, (S, 8), generator=g).to(gpu)
+    weights = torch.softmax(torch.randn(S, 8, generator=g), -1).to(gpu)
+    calls = [lambda: fused_moe(x, index, weights, *st),
+             lambda: fused_moe(x, index, weights, gq, gs, None, dq, ds, None)]
+    with torch.no_grad():
+        for call in calls:
+            monkeypatch.setenv("JANUS_MOE_SCHEDULE", "split")
+            split = call().clone()
+            monkeypatch.delenv("JANUS_MOE_SCHEDULE")
+            for _ in range(2):
+                out = call()
+                torch.cuda.synchronize()
+                assert torch.equal(out, split)
+
+
 def test_block_graph_captured_first_in_a_fresh_thread(gpu):
     """The first block call of a fresh thread is the capture itself (torch's per-thread current stream, a new
     allocator pool); replays still match eager execution."""
