@@ -1,8 +1,9 @@
 """The MoE slice of janus/hybrid.py (:395-701): two weight codecs and their modules, and `moe_kernel` (the
 JANUS_MOE_KERNEL switch).
-  - int4 group-128 (this port's headline codec): `W4A16Linear`, `W4A16Experts`.
+  - int4 group-128 (the headline codec): `W4A16Linear`, `W4A16Experts`, and `repack_int4` from NVFP4.
   - NVFP4 (the reference's ModelOpt checkpoint format, janus/hybrid.py:395-451): `nvfp4_quantize` /
-    `nvfp4_dequantize`, `NVFP4Linear`, `NVFP4Experts`, same names, buffers and forward signatures as the reference.
+    `nvfp4_dequantize`, `NVFP4Linear`, `NVFP4Experts`, same names, buffers and forward signatures as the reference,
+    and `load_nvfp4` (janus/hybrid.py:641-701) from a ModelOpt checkpoint into them.
 
 Dispatch follows janus/hybrid.py:551-572: under inference on a GPU the experts run the fused HIP kernels
 (`moe_w4a16.fused_moe`); with gradients enabled or on the CPU the stacks are dequantised per call and run through
@@ -331,3 +332,133 @@ class NVFP4Experts(_PackedExperts):
     @property
     def down_proj(self) -> torch.Tensor:
         return nvfp4_dequantize(self.down, self.down_scale, self.down_global, torch.bfloat16)
+
+
+# ---- load / repack (janus/hybrid.py:641-701) -------------------------------------------------------------------
+
+MODEL_PREFIX = "model.language_model."
+
+
+def load_nvfp4(lm, snapshot, dtype=torch.bfloat16):
+    """Fill a meta-device Qwen3_5MoeTextModel `lm` from a ModelOpt NVFP4 checkpoint directory, as
+    janus/hybrid.py:641-701 does. The checkpoint keeps each expert's `gate_proj`/`up_proj`/`down_proj` as NVFP4
+    (`weight` uint8 pairs, `weight_scale` e4m3 per 16, `weight_scale_2` one fp32), the shared expert's linears likewise,
+    the attention and linear-attention projections as fp8 e4m3 with one fp32 `weight_scale`, and everything else in
+    bf16.
+      - every layer's experts become `NVFP4Experts` with stacks allocated before `to_empty` (so no bf16 stack ever
+        exists) and filled per expert: gate rows 0..I-1, up rows I..2I-1, each projection's `weight_scale_2` spread over
+        its rows (the shape table of janus/hybrid.py:658-660);
+      - NVFP4 linears become `NVFP4Linear`, packed as stored; fp8 projections are dequantised once to `dtype`;
+      - `input_scale` (activation calibration) is not used, and keys outside `model.language_model.` (vision tower,
+        MTP head, lm_head) are skipped.
+    Shards are read on the CPU. Raises ValueError when a model parameter, or a piece of an expert stack, is left
+    unfilled."""
+    import json
+    from pathlib import Path
+
+    from safetensors import safe_open
+
+    snapshot = Path(snapshot)
+    weight_map = json.loads((snapshot / "model.safetensors.index.json").read_text())["weight_map"]
+    cfg = lm.config
+    E, I, H = cfg.num_experts, cfg.moe_intermediate_size, cfg.hidden_size
+    for layer in lm.layers:
+        act = layer.mlp.experts.act_fn
+        e4m3 = torch.float8_e4m3fn
+        layer.mlp.experts = NVFP4Experts(
+            torch.empty(E, 2 * I, H // 2, dtype=torch.uint8), torch.empty(E, 2 * I, H // FP4_BLOCK, dtype=e4m3),
+            torch.empty(E, 2 * I, 1), torch.empty(E, H, I // 2, dtype=torch.uint8),
+            torch.empty(E, H, I // FP4_BLOCK, dtype=e4m3), torch.empty(E, H, 1), act)
+    lm.to_empty(device="cpu")
+    lm.rotary_emb = type(lm.rotary_emb)(config=cfg)  # its inv_freq buffers are not persistent: to_empty left them empty
+    modules = dict(lm.named_modules())
+
+    shards: dict[str, list[str]] = {}
+    for key, shard in weight_map.items():
+        if key.startswith(MODEL_PREFIX):
+            shards.setdefault(shard, []).append(key[len(MODEL_PREFIX):])
+    filled, expert_pieces, quantised = set(), set(), {}
+    stack_of = {"weight": ("gate_up", "down"), "weight_scale": ("gate_up_scale", "down_scale"),
+                "weight_scale_2": ("gate_up_global", "down_global")}
+    for shard in sorted(shards):
+        with safe_open(str(snapshot / shard), "pt", device="cpu") as f:
+            for name in sorted(shards[shard]):
+                module, _, leaf = name.rpartition(".")
+                if leaf == "input_scale":
+                    continue
+                t = f.get_tensor(MODEL_PREFIX + name)
+                if ".mlp.experts." in module:
+                    owner, _, rest = module.rpartition(".experts.")
+                    index, proj = rest.split(".")
+                    experts = modules[owner + ".experts"]
+                    gu_name, dn_name = stack_of[leaf]
+                    if proj == "down_proj":
+                        dst = getattr(experts, dn_name)[int(index)]
+                    else:
+                        rows = slice(0, I) if proj == "gate_proj" else slice(I, 2 * I)
+                        dst = getattr(experts, gu_name)[int(index), rows]
+                    dst.copy_(t.reshape(()).expand(dst.shape) if leaf == "weight_scale_2" else t)
+                    expert_pieces.add((owner, int(index), proj, leaf))
+                elif leaf in ("weight_scale", "weight_scale_2") or t.dtype in (torch.uint8, torch.float8_e4m3fn):
+                    quantised.setdefault(module, {})[leaf] = t
+                else:
+                    getattr(modules[module], leaf).data = t.to(dtype)
+                    filled.add(name)
+    incomplete = []
+    for module, parts in quantised.items():
+        owner, _, leaf = module.rpartition(".")
+        nvfp4 = "weight_scale_2" in parts or ("weight" in parts and parts["weight"].dtype == torch.uint8)
+        need = ("weight", "weight_scale", "weight_scale_2") if nvfp4 else ("weight", "weight_scale")
+        if any(n not in parts for n in need):
+            incomplete += [f"{module}.{n}" for n in need if n not in parts]
+            continue
+        if parts["weight"].dtype == torch.uint8:  # NVFP4: kept packed, the nn.Linear replaced
+            setattr(modules[owner], leaf, NVFP4Linear(parts["weight"], parts["weight_scale"], parts["weight_scale_2"]))
+        else:  # fp8 with one fp32 scale: dequantised once
+            modules[module].weight.data = (parts["weight"].float() * parts["weight_scale"].float()).to(dtype)
+            filled.add(module + ".weight")
+
+    missing = incomplete + [n for n, _ in lm.named_parameters() if n not in filled]
+    pieces = [(p, leaf) for p in ("gate_proj", "up_proj", "down_proj") for leaf in ("weight", "weight_scale",
+                                                                                   "weight_scale_2")]
+    for i in range(len(lm.layers)):
+        owner = f"layers.{i}.mlp"
+        missing += [f"{owner}.experts.{e}.{p}.{leaf}" for e in range(E) for p, leaf in pieces
+                    if (owner, e, p, leaf) not in expert_pieces]
+    if missing:
+        raise ValueError(f"{snapshot}: {len(missing)} model tensors not in the shards, e.g. {missing[:5]}")
+    return lm
+
+
+def _nvfp4_to_int4(packed, scale, global_scale):
+    """One NVFP4 matrix [N, K/2] to the int4 group-128 codec: the NVFP4 decode (bf16, the reference's rule), then
+    symmetric group-128 quantisation (int4_quantize)."""
+    return int4_quantize(nvfp4_dequantize(packed, scale, global_scale, torch.bfloat16).float())
+
+
+def repack_int4(module: nn.Module) -> nn.Module:
+    """The int4 group-128 repacker: every NVFP4Experts / NVFP4Linear under `module` (itself included) is replaced by
+    W4A16Experts / W4A16Linear holding the NVFP4 weights decoded to bf16 and requantised per 128 k (scale
+    bf16(amax / 7)). Expert stacks go one expert at a time, so no bf16 stack is held. Lossy, as any change of codec:
+    each group's 16 uniform levels replace the e2m1 grid under per-16 scales. Returns the module (or its
+    replacement when `module` itself is packed)."""
+    def convert(m):
+        if isinstance(m, NVFP4Linear):
+            words, scales = _nvfp4_to_int4(m.packed, m.scale, m.global_scale)
+            return W4A16Linear(words, scales)
+        if isinstance(m, NVFP4Experts):
+            gu = [_nvfp4_to_int4(m.gate_up[e], m.gate_up_scale[e], m.gate_up_global[e]) for e in range(m.num_experts)]
+            dn = [_nvfp4_to_int4(m.down[e], m.down_scale[e], m.down_global[e]) for e in range(m.num_experts)]
+            return W4A16Experts(torch.stack([w for w, _ in gu]), torch.stack([s for _, s in gu]), None,
+                                torch.stack([w for w, _ in dn]), torch.stack([s for _, s in dn]), None, m.act_fn)
+        return None
+
+    top = convert(module)
+    if top is not None:
+        return top
+    for name, child in list(module.named_modules()):
+        new = convert(child)
+        if new is not None:
+            owner, _, leaf = name.rpartition(".")
+            setattr(module.get_submodule(owner) if owner else module, leaf, new)
+    return module
