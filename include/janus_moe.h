@@ -155,6 +155,16 @@ JANUS_MOE_API size_t janus_moe_block_workspace_bytes(int T, int H, int I, int E,
 JANUS_MOE_API int janus_moe_block_forward(const janus_moe_block_weights* w, const uint16_t* x, int T, uint16_t* out,
                             int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------------------
+ * janus_moe_block_forward over a level batch with right padding: the caller's `valid` mask (janus/hybrid.py:
+ * 1730-1745 builds it per level, [rows, length] bool, False = padding) flattened to [T] bytes, nonzero = a real
+ * token. Padding tokens are routed to no expert (topk_idx = E, topk_w = 0), so the expert GEMMs skip their rows, and
+ * their output rows are zero; real tokens get bit for bit the unmasked result. valid NULL = every token. Device
+ * memory, read on the stream, so a captured graph replays with whatever mask the buffer holds. */
+JANUS_MOE_API int janus_moe_block_forward_masked(const janus_moe_block_weights* w, const uint16_t* x,
+                                                 const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                                 float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -110,9 +110,15 @@ class W4A16SparseMoeBlock(nn.Module):
             shared_gate.weight.requires_grad_(False)
         return cls(router, experts, shared, shared_gate)
 
-    def forward(self, hidden_states):
+    def forward(self, hidden_states, valid=None):
+        """hidden_states [..., H]. valid: optional bool mask of hidden_states' leading shape (a level batch's
+        [rows, length] right-padding mask, janus/hybrid.py:1730-1745), False = padding: those tokens go to no expert
+        and their output rows are zero; the other rows equal the unmasked forward."""
         shape = hidden_states.shape
         x = hidden_states.reshape(-1, shape[-1])
+        keep = None if valid is None else valid.reshape(-1)
+        if keep is not None and keep.shape[0] != x.shape[0]:
+            raise ValueError(f"valid has {keep.shape[0]} entries for {x.shape[0]} tokens")
         if x.is_cuda and not torch.is_grad_enabled() and moe_kernel(x.device) == "fused":
             sh = self.shared_expert
             out, _, _ = ops.block_forward(
@@ -122,7 +128,7 @@ class W4A16SparseMoeBlock(nn.Module):
                 None if sh is None else sh.down, None if sh is None else sh.down_scale,
                 None if self.shared_expert_gate is None else
                 self.shared_expert_gate.weight.reshape(-1).to(torch.bfloat16).contiguous(),
-                self.gate.top_k)
+                self.gate.top_k, None if keep is None else keep.to(torch.bool).contiguous())
             return out.to(hidden_states.dtype).reshape(shape)
         _, weights, idx = self.gate(x)
         out = self.experts(x, idx, weights.to(x.dtype))
@@ -131,4 +137,6 @@ class W4A16SparseMoeBlock(nn.Module):
             if self.shared_expert_gate is not None:
                 shared = torch.sigmoid(self.shared_expert_gate(x)) * shared
             out = out + shared
+        if keep is not None:
+            out = torch.where(keep.to(out.device, torch.bool)[:, None], out, torch.zeros_like(out))
         return out.reshape(shape)

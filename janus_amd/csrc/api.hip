@@ -80,7 +80,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
                 const int32_t* dq, const uint16_t* ds, const int32_t* sguq, const uint16_t* sgus, const int32_t* sdq,
                 const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
                 const ExpertsWorkspace& w, hipStream_t stream, int codec = 0, const float* gu_global = nullptr,
-                const float* dn_global = nullptr) {
+                const float* dn_global = nullptr, const uint8_t* valid = nullptr) {
   const int A = T * top_k;
   mark(1, stream);
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
@@ -141,7 +141,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   }
   if (rc) return rc;
   mark(4, stream);
-  rc = launch_combine(w.slots, w.nslots, out, T, H, stream);
+  rc = launch_combine(w.slots, w.nslots, out, T, H, valid, stream);
   mark(5, stream);
   return rc;
 }
@@ -249,6 +249,12 @@ extern "C" size_t janus_moe_block_workspace_bytes(int T, int H, int I, int E, in
 extern "C" int janus_moe_block_forward(const janus_moe_block_weights* wt, const uint16_t* x, int T, uint16_t* out,
                                        int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes,
                                        janus_stream_t stream) {
+  return janus_moe_block_forward_masked(wt, x, nullptr, T, out, topk_idx, topk_w, ws, ws_bytes, stream);
+}
+
+extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt, const uint16_t* x,
+                                              const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                              float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream) {
   JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward: null weights");
   const int H = wt->H, I = wt->I, E = wt->E, k = wt->top_k, I_s = wt->I_s;
   int rc = check_expert_sizes("janus_moe_block_forward", T, H, I, E, k);
@@ -270,12 +276,12 @@ extern "C" int janus_moe_block_forward(const janus_moe_block_weights* wt, const 
   float* rw = topk_w ? topk_w : b.topk_w;
   const bool gated = I_s > 0 && wt->sh_gate_w;
   mark(0, (hipStream_t)stream);
-  rc = launch_route(x, wt->router_w, wt->router_prep, wt->router_bias, gated ? wt->sh_gate_w : nullptr, T, H, E, k, idx,
-                    rw, b.gamma, b.route, (hipStream_t)stream);
+  rc = launch_route(x, wt->router_w, wt->router_prep, wt->router_bias, gated ? wt->sh_gate_w : nullptr, T, H, E, k,
+                    valid, idx, rw, b.gamma, b.route, (hipStream_t)stream);
   if (rc) return rc;
   return run_experts<int>(x, idx, rw, wt->gate_up_q, wt->gate_up_s, wt->down_q, wt->down_s, wt->sh_gate_up_q,
                           wt->sh_gate_up_s, wt->sh_down_q, wt->sh_down_s, gated ? b.gamma : nullptr, T, H, I, I_s, E, k,
-                          out, b.experts, (hipStream_t)stream);
+                          out, b.experts, (hipStream_t)stream, 0, nullptr, nullptr, valid);
 }
 
 extern "C" int janus_moe_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out,

@@ -53,8 +53,10 @@ constexpr int kNotFused = 1;  // launch_experts_fused: no persistent kernel for 
 int launch_experts_fused(const GemmParams& gu, const GemmParams& dn, int* sched, hipStream_t stream);
 int launch_gate_up(const GemmParams& p, hipStream_t stream);
 int launch_down(const GemmParams& p, hipStream_t stream);
-// out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32.
-int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, hipStream_t stream);
+// out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32; 0 where valid[t] == 0 (valid null:
+// every token).
+int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, const uint8_t* valid,
+                   hipStream_t stream);
 int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream);
 int launch_dequant_nvfp4(const uint8_t* q, const uint8_t* s, const float* gs, long rows, int K, uint16_t* out,
                          hipStream_t stream);

@@ -464,12 +464,17 @@ __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmPara
 }
 
 // out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order. The loads of up to 8 slots
-// are issued together before the additions.
-__global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4) {
+// are issued together before the additions. A padding token (valid[t] == 0) gets zeros and its slots are not read.
+__global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4,
+                               const uint8_t* __restrict__ valid) {
   constexpr int kBatch = 8;
   const long n = (long)T * H4;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
     const long t = i / H4, col = i - t * H4;
+    if (valid && !valid[t]) {
+      out[i] = make_uint2(0u, 0u);
+      continue;
+    }
     const float4* src = slots + t * nslots * H4 + col;
     float4 s = src[0];
     for (int j0 = 1; j0 < nslots; j0 += kBatch) {
@@ -607,13 +612,14 @@ int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* 
 int launch_gate_up(const GemmParams& p, hipStream_t stream) { return launch_gemm<kGateUp>(p, stream); }
 int launch_down(const GemmParams& p, hipStream_t stream) { return launch_gemm<kDown>(p, stream); }
 
-int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, hipStream_t stream) {
+int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, const uint8_t* valid,
+                   hipStream_t stream) {
   const long n4 = (long)T * (H / 4);
   if (n4 == 0) return JANUS_MOE_OK;
   long blocks = (n4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, reinterpret_cast<const float4*>(slots),
-                     nslots, reinterpret_cast<uint2*>(out), T, H / 4);
+                     nslots, reinterpret_cast<uint2*>(out), T, H / 4, valid);
   JANUS_LAUNCH_CHECK("combine");
   return JANUS_MOE_OK;
 }

@@ -372,14 +372,23 @@ template <int NHV, int NJ>
 __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ w, RouterPrep p, const float* __restrict__ bias,
     const uint16_t* __restrict__ wsg, int T, int H, int E, int Epad, int nslice, int top_k,
-    const float* __restrict__ partial, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
-    float* __restrict__ gamma) {
+    const float* __restrict__ partial, const uint8_t* __restrict__ valid, int32_t* __restrict__ topk_idx,
+    float* __restrict__ topk_w, float* __restrict__ gamma) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   Cand* cand = reinterpret_cast<Cand*>(smem) + (size_t)wave * 2 * E;
   Cand* sorted = cand + E;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;  // a whole wave; no workgroup barriers below
+  if (valid && !valid[t]) {
+    // a padding token: no expert (id E is dropped by align), weight 0, shared-expert gate 0
+    if (lane < top_k) {
+      topk_idx[(long)t * top_k + lane] = E;
+      topk_w[(long)t * top_k + lane] = 0.f;
+    }
+    if (lane == 0 && gamma) gamma[t] = 0.f;
+    return;
+  }
 
   // every load up front: x row, shared-gate row, approximate logit slices, bias
   XRow<NHV> xrow;
@@ -590,8 +599,8 @@ RouteWorkspace carve_route(Carver& c, int T, int H, int E) {
 }
 
 int launch_route(const uint16_t* x, const float* w, const void* prep, const float* bias, const uint16_t* wsg, int T,
-                 int H, int E, int top_k, int32_t* topk_idx, float* topk_w, float* gamma, const RouteWorkspace& ws,
-                 hipStream_t stream) {
+                 int H, int E, int top_k, const uint8_t* valid, int32_t* topk_idx, float* topk_w, float* gamma,
+                 const RouteWorkspace& ws, hipStream_t stream) {
   if (T == 0) return JANUS_MOE_OK;
   Carver pc(const_cast<void*>(prep));
   RouterPrep p = carve_prep(pc, E, H);
@@ -605,7 +614,7 @@ int launch_route(const uint16_t* x, const float* w, const void* prep, const floa
   const int nhv = ceil_div(H, 512), nj = ceil_div(E, 64);
 #define JANUS_SELECT(NHV_, NJ_)                                                                                   \
   hipLaunchKernelGGL((router_select_kernel<NHV_, NJ_>), sg, sb, smem, stream, x, w, p, bias, wsg, T, H, E, Epad, \
-                     nslice, top_k, ws.partial, topk_idx, topk_w, gamma)
+                     nslice, top_k, ws.partial, valid, topk_idx, topk_w, gamma)
 #define JANUS_SELECT_NJ(NHV_)       \
   if (nj <= 2)                      \
     JANUS_SELECT(NHV_, 2);          \
@@ -676,6 +685,6 @@ extern "C" int janus_moe_route(const uint16_t* x, const float* w_router, const v
                 need);
   Carver c(ws);
   RouteWorkspace r = carve_route(c, T, H, E);
-  return launch_route(x, w_router, prep, bias, w_shared_gate, T, H, E, top_k, topk_idx, topk_w, gamma, r,
+  return launch_route(x, w_router, prep, bias, w_shared_gate, T, H, E, top_k, nullptr, topk_idx, topk_w, gamma, r,
                       (hipStream_t)stream);
 }

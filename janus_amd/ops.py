@@ -276,9 +276,11 @@ def _(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, dow
 def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias: Optional[Tensor], gate_up_q: Tensor,
                   gate_up_s: Tensor, down_q: Tensor, down_s: Tensor, sh_gate_up_q: Optional[Tensor],
                   sh_gate_up_s: Optional[Tensor], sh_down_q: Optional[Tensor], sh_down_s: Optional[Tensor],
-                  sh_gate_w: Optional[Tensor], top_k: int) -> tuple[Tensor, Tensor, Tensor]:
+                  sh_gate_w: Optional[Tensor], top_k: int,
+                  valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
     """Router + routed experts + gated shared expert, one fp32 sum rounded once: (out [T, H] bf16, indices [T, k]
-    int32, weights [T, k] fp32)."""
+    int32, weights [T, k] fp32). valid: optional [T] bool (or uint8), False = a padding token: routed to no expert
+    (index E, weight 0) and given a zero output row; the other rows are the unmasked result bit for bit."""
     dev = _require_gpu(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s, sh_gate_up_q,
                        sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w)
     T, H = x.shape
@@ -293,6 +295,12 @@ def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias:
     _expect(down_s, "down_s", torch.bfloat16, (E, H, I // 128))
     if router_bias is not None:
         _expect(router_bias, "router_bias", torch.float32, (E,))
+    if valid is not None:
+        if valid.dtype not in (torch.bool, torch.uint8) or tuple(valid.shape) != (T,) or not valid.is_contiguous():
+            raise ValueError(f"valid: expected a contiguous bool or uint8 [{T}] tensor, got {valid.dtype} "
+                             f"{tuple(valid.shape)}")
+        if valid.device != dev:
+            raise ValueError(f"valid is on {valid.device}, x on {dev}")
     I_s = 0
     if sh_gate_up_q is not None:
         I_s = sh_gate_up_q.shape[0] // 2
@@ -312,13 +320,13 @@ def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias:
     n = L.janus_moe_block_workspace_bytes(T, H, I, E, top_k, I_s)
     ws = _workspace(n, dev)
     with torch.cuda.device(dev):
-        check(L.janus_moe_block_forward(ctypes.byref(weights), _ptr(x), T, _ptr(out), _ptr(idx), _ptr(rw), _ptr(ws),
-                                        ws.numel(), _stream(dev)), "janus_moe_block_forward")
+        check(L.janus_moe_block_forward_masked(ctypes.byref(weights), _ptr(x), _ptr(valid), T, _ptr(out), _ptr(idx),
+                                               _ptr(rw), _ptr(ws), ws.numel(), _stream(dev)), "janus_moe_block_forward")
     return out, idx, rw
 
 
 @block_forward.register_fake
 def _(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s, sh_gate_up_q, sh_gate_up_s,
-      sh_down_q, sh_down_s, sh_gate_w, top_k):
+      sh_down_q, sh_down_s, sh_gate_w, top_k, valid=None):
     T = x.shape[0]
     return (torch.empty_like(x), x.new_empty(T, top_k, dtype=torch.int32), x.new_empty(T, top_k, dtype=torch.float32))

@@ -244,6 +244,53 @@ def test_block_graph_replay_matches_eager(gpu):
     _replays_match_eager(blk, x)
 
 
+def _padding_mask(T, rows, seed):
+    """A level batch's right-padding mask (janus/hybrid.py:1730-1745): `rows` rows of T / rows positions, row lengths
+    drawn in [0, length] with an empty and a full row."""
+    length = T // rows
+    lengths = torch.randint(0, length + 1, (rows,), generator=torch.Generator().manual_seed(seed))
+    lengths[0], lengths[-1] = 0, length
+    return (torch.arange(length)[None] < lengths[:, None]).reshape(-1)
+
+
+@pytest.mark.parametrize("name,rows", [("tiny", 4), ("short", 4), ("headline", 8)])
+def test_block_valid_mask_skips_padding_rows(gpu, name, rows):
+    """The valid-mask row skip: padding tokens are routed to no expert (index E, weight 0) and get zero rows; every
+    real token's row is the unmasked forward bit for bit. A captured graph replays with the mask rewritten in place."""
+    cfg = synth.CONFIGS[name]
+    _, blk = _block(cfg, gpu)
+    x = synth.activations(cfg).to(gpu)
+    sh = blk.shared_expert
+    with torch.no_grad():
+        full = blk(x).clone()
+        valid = _padding_mask(cfg.T, rows, seed=rows).to(gpu)
+        out = blk(x, valid=valid)
+        torch.cuda.synchronize()
+        assert torch.equal(out[valid], full[valid])
+        assert not out[~valid].any()
+        _, idx, w = ops.block_forward(
+            x, blk.gate.weight, blk.gate.prep(), blk.gate.bias, blk.experts.gate_up, blk.experts.gate_up_scale,
+            blk.experts.down, blk.experts.down_scale, None if sh is None else sh.gate_up,
+            None if sh is None else sh.gate_up_scale, None if sh is None else sh.down,
+            None if sh is None else sh.down_scale,
+            None if blk.shared_expert_gate is None else blk.shared_expert_gate.weight.reshape(-1).bfloat16().contiguous(),
+            cfg.k, valid)
+        assert torch.all(idx[~valid] == cfg.E) and not w[~valid].any()
+        assert torch.all(idx[valid] < cfg.E)
+        # graph: one capture, masks swapped in the same buffer between replays
+        vbuf = valid.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = blk(x, valid=vbuf)
+        for seed in (11, 12, 13):
+            mask = _padding_mask(cfg.T, rows, seed).to(gpu)
+            vbuf.copy_(mask)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(captured, blk(x, valid=mask))
+            assert torch.equal(captured[mask], full[mask])
+
+
 @pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf"])
 def test_persistent_schedule_equals_one_launch_per_gemm(gpu, name, monkeypatch):
     """Both GEMMs in one persistent launch (a ticket queue per XCD, down units waiting for their chunk's gate_up

@@ -207,6 +207,20 @@ def test_cpu_block_matches_oracle():
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
 
 
+def test_cpu_block_valid_mask_zeroes_padding_rows():
+    """The torch path of the valid mask: [rows, length] right padding, real rows as without the mask, padding rows
+    zero; a mask of the wrong size raises."""
+    cfg = synth.CONFIGS["tiny"]
+    blk = W4A16SparseMoeBlock.from_tensors(synth.layer(cfg), cfg.k)
+    x = synth.activations(cfg).reshape(4, cfg.T // 4, cfg.H)
+    valid = torch.arange(cfg.T // 4)[None] < torch.tensor([0, 5, 17, cfg.T // 4])[:, None]
+    with torch.no_grad():
+        full, out = blk(x), blk(x, valid=valid)
+    assert torch.equal(out[valid], full[valid]) and not out[~valid].any()
+    with pytest.raises(ValueError):
+        blk(x, valid=valid[:, :-1])
+
+
 def test_cpu_baseline_port_matches_oracle():
     """oracle/cpu_bmm.py, the reference's CPU algorithm that bench.py times, computes the same layer (bf16-rounded
     like the reference) on the tiny config."""
