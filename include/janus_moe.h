@@ -165,6 +165,30 @@ JANUS_MOE_API int janus_moe_block_forward_masked(const janus_moe_block_weights* 
                                                  const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
                                                  float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------------------
+ * Replaces _add_norm (janus/hybrid.py:267-273, with _rmsnorm :250-254): x_out = residual + h in bf16 (torch's bf16 add:
+ * the fp32 sum rounded once; h NULL = no add) and n_out = Qwen3_5RMSNorm(x_out) =
+ * bf16(fp32(x) * rsqrt(mean(fp32(x)^2) + eps) * (1 + fp32(weight))), zeroed where valid[t] == 0 (valid NULL: no mask).
+ * [T, H] bf16 rows, weight [H] bf16; H % 4 == 0, H <= 4096. x_out may be NULL or alias residual; n_out may alias h. */
+JANUS_MOE_API int janus_moe_add_rmsnorm(const uint16_t* residual, const uint16_t* h, const uint16_t* weight, float eps,
+                                        const uint8_t* valid, int T, int H, uint16_t* x_out, uint16_t* n_out,
+                                        janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
+ * The MoE layer with its serving neighbours (janus/hybrid.py:1096-1105, `_serve_level`): the post-attention
+ * _add_norm, the block, and the next _add_norm with the block's output as its h, which replaces
+ *   x1, n1 = _add_norm(x, h_attn, post_norm_w, post_eps, None);  moe = block(n1);
+ *   x_out, h_out = _add_norm(x1, moe, next_norm_w, next_eps, next_valid)
+ * with the combine writing the second _add_norm directly (the MoE output is never stored). valid (NULL: none) skips
+ * padding tokens in the block as janus_moe_block_forward_masked does (their moe is 0). x_out may alias x; h_out must
+ * alias neither; h_attn may alias h_out. Workspace: janus_moe_block_workspace_bytes. */
+JANUS_MOE_API int janus_moe_block_forward_serve(const janus_moe_block_weights* w, const uint16_t* x,
+                                                const uint16_t* h_attn, const uint16_t* post_norm_w, float post_eps,
+                                                const uint16_t* next_norm_w, float next_eps, const uint8_t* valid,
+                                                const uint8_t* next_valid, int T, uint16_t* x_out, uint16_t* h_out,
+                                                int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes,
+                                                janus_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

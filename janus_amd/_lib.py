@@ -20,6 +20,7 @@ EXPORTS = (
     "janus_moe_align_workspace_bytes", "janus_moe_align",
     "janus_moe_experts_workspace_bytes", "janus_moe_experts",
     "janus_moe_block_workspace_bytes", "janus_moe_block_forward", "janus_moe_block_forward_masked",
+    "janus_moe_add_rmsnorm", "janus_moe_block_forward_serve",
     "janus_moe_dequant", "janus_moe_profile_events",
     "janus_moe_experts_nvfp4", "janus_moe_dequant_nvfp4",
 )
@@ -52,6 +53,9 @@ _SIGNATURES = {
     "janus_moe_block_workspace_bytes": (_z, [_i, _i, _i, _i, _i, _i]),
     "janus_moe_block_forward": (_i, [ctypes.POINTER(BlockWeights), _p, _i, _p, _p, _p, _p, _z, _p]),
     "janus_moe_block_forward_masked": (_i, [ctypes.POINTER(BlockWeights), _p, _p, _i, _p, _p, _p, _p, _z, _p]),
+    "janus_moe_add_rmsnorm": (_i, [_p, _p, _p, ctypes.c_float, _p, _i, _i, _p, _p, _p]),
+    "janus_moe_block_forward_serve": (_i, [ctypes.POINTER(BlockWeights), _p, _p, _p, ctypes.c_float, _p,
+                                           ctypes.c_float, _p, _p, _i, _p, _p, _p, _p, _p, _z, _p]),
     "janus_moe_dequant": (_i, [_p, _p, ctypes.c_long, _i, _p, _p]),
     "janus_moe_profile_events": (_i, [ctypes.POINTER(_p), _i]),
     "janus_moe_experts_nvfp4": (_i, [_p] * 9 + [_i] * 5 + [_p, _p, _z, _p]),

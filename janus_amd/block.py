@@ -140,3 +140,35 @@ class W4A16SparseMoeBlock(nn.Module):
         if keep is not None:
             out = torch.where(keep.to(out.device, torch.bool)[:, None], out, torch.zeros_like(out))
         return out.reshape(shape)
+
+    def serve(self, x, h_attn, post_norm, next_norm, valid=None, next_valid=None):
+        """The layer between its serving neighbours (janus/hybrid.py:1096-1105, `_serve_level`):
+            x1, n1 = _add_norm(x, h_attn, post_norm); moe = self(n1, valid); return _add_norm(x1, moe, next_norm,
+            next_valid)
+        x, h_attn [..., H] bf16 (h_attn None: no add); post_norm / next_norm are Qwen3_5RMSNorm modules (`weight`,
+        `eps`); valid / next_valid optional bool masks of x's leading shape. Returns (x_out, h_out) shaped like x.
+        Under inference on a GPU it is one janus_moe::block_forward_serve call, whose combine kernel writes the second
+        _add_norm directly; otherwise the same composition in torch."""
+        shape = x.shape
+        flat = lambda t: None if t is None else t.reshape(-1, shape[-1])
+        mask = lambda m: None if m is None else m.reshape(-1).to(torch.bool).contiguous()
+        if x.is_cuda and not torch.is_grad_enabled() and moe_kernel(x.device) == "fused" and x.dtype == torch.bfloat16:
+            sh = self.shared_expert
+            x_out, h_out = ops.block_forward_serve(
+                flat(x).contiguous(), None if h_attn is None else flat(h_attn).contiguous(),
+                post_norm.weight.detach().to(torch.bfloat16).contiguous(), float(post_norm.eps),
+                next_norm.weight.detach().to(torch.bfloat16).contiguous(), float(next_norm.eps),
+                self.gate.weight, self.gate.prep(), self.gate.bias, self.experts.gate_up, self.experts.gate_up_scale,
+                self.experts.down, self.experts.down_scale, None if sh is None else sh.gate_up,
+                None if sh is None else sh.gate_up_scale, None if sh is None else sh.down,
+                None if sh is None else sh.down_scale,
+                None if self.shared_expert_gate is None else
+                self.shared_expert_gate.weight.reshape(-1).to(torch.bfloat16).contiguous(),
+                self.gate.top_k, mask(valid), mask(next_valid))
+            return x_out.reshape(shape), h_out.reshape(shape)
+        x1 = x if h_attn is None else x + h_attn
+        x2 = x1 + self(post_norm(x1), valid)
+        h = next_norm(x2)
+        if next_valid is not None:
+            h = torch.where(next_valid.reshape(*shape[:-1], 1).to(h.device, torch.bool), h, torch.zeros_like(h))
+        return x2, h

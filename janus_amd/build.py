@@ -18,7 +18,7 @@ ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libjanus_moe_hip.so"
-SOURCES = ("align.hip", "router.hip", "gemm.hip", "api.hip")
+SOURCES = ("align.hip", "router.hip", "gemm.hip", "norm.hip", "api.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -9,6 +9,7 @@
 
 #include "align.h"
 #include "gemm.h"
+#include "norm.h"
 #include "router.h"
 
 namespace janus {
@@ -74,13 +75,24 @@ int check_expert_sizes(const char* who, int T, int H, int I, int E, int top_k) {
   return JANUS_MOE_OK;
 }
 
+// The serving epilogue of run_experts: instead of writing the MoE output, add it to the residual x_res in place and
+// write the next layer's normed input n_out (0 where valid[t] == 0).
+struct ServeEpilogue {
+  uint16_t* x_res;
+  const uint16_t* norm_w;
+  float eps;
+  const uint8_t* valid;
+  uint16_t* n_out;
+};
+
 // Runs align + the two grouped GEMMs + the combine; routing (idx, weights) already on the device.
 template <typename IdxT>
 int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const int32_t* guq, const uint16_t* gus,
                 const int32_t* dq, const uint16_t* ds, const int32_t* sguq, const uint16_t* sgus, const int32_t* sdq,
                 const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
                 const ExpertsWorkspace& w, hipStream_t stream, int codec = 0, const float* gu_global = nullptr,
-                const float* dn_global = nullptr, const uint8_t* valid = nullptr) {
+                const float* dn_global = nullptr, const uint8_t* valid = nullptr,
+                const ServeEpilogue* serve = nullptr) {
   const int A = T * top_k;
   mark(1, stream);
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
@@ -141,7 +153,11 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   }
   if (rc) return rc;
   mark(4, stream);
-  rc = launch_combine(w.slots, w.nslots, out, T, H, valid, stream);
+  if (serve)  // the combine folded into the next residual add + norm; `out` is not written
+    rc = launch_combine_add_rmsnorm(w.slots, w.nslots, valid, serve->x_res, serve->norm_w, serve->eps, serve->valid,
+                                    T, H, serve->n_out, stream);
+  else
+    rc = launch_combine(w.slots, w.nslots, out, T, H, valid, stream);
   mark(5, stream);
   return rc;
 }
@@ -252,9 +268,11 @@ extern "C" int janus_moe_block_forward(const janus_moe_block_weights* wt, const 
   return janus_moe_block_forward_masked(wt, x, nullptr, T, out, topk_idx, topk_w, ws, ws_bytes, stream);
 }
 
-extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt, const uint16_t* x,
-                                              const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
-                                              float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream) {
+namespace {
+// The block forward behind the three block entries: x is the MoE input; serve null writes the layer output to out.
+int block_forward(const janus_moe_block_weights* wt, const uint16_t* x, const uint8_t* valid, int T, uint16_t* out,
+                  int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes, hipStream_t stream,
+                  const ServeEpilogue* serve) {
   JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward: null weights");
   const int H = wt->H, I = wt->I, E = wt->E, k = wt->top_k, I_s = wt->I_s;
   int rc = check_expert_sizes("janus_moe_block_forward", T, H, I, E, k);
@@ -264,8 +282,9 @@ extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt,
   JANUS_REQUIRE(I_s >= 0 && I_s % 128 == 0, JANUS_MOE_EINVAL, "janus_moe_block_forward: I_s=%d must be a multiple of 128",
                 I_s);
   if (T == 0) return JANUS_MOE_OK;
-  JANUS_REQUIRE(x && out && wt->router_w && wt->router_prep && wt->gate_up_q && wt->gate_up_s && wt->down_q &&
-                    wt->down_s && (I_s == 0 || (wt->sh_gate_up_q && wt->sh_gate_up_s && wt->sh_down_q && wt->sh_down_s)),
+  JANUS_REQUIRE(x && (out || serve) && wt->router_w && wt->router_prep && wt->gate_up_q && wt->gate_up_s &&
+                    wt->down_q && wt->down_s &&
+                    (I_s == 0 || (wt->sh_gate_up_q && wt->sh_gate_up_s && wt->sh_down_q && wt->sh_down_s)),
                 JANUS_MOE_EINVAL, "janus_moe_block_forward: null pointer");
   const size_t need = janus_moe_block_workspace_bytes(T, H, I, E, k, I_s);
   JANUS_REQUIRE(ws && ws_bytes >= need, JANUS_MOE_EWORKSPACE, "janus_moe_block_forward: workspace %zu < %zu bytes",
@@ -275,13 +294,43 @@ extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt,
   int32_t* idx = topk_idx ? topk_idx : b.topk_idx;
   float* rw = topk_w ? topk_w : b.topk_w;
   const bool gated = I_s > 0 && wt->sh_gate_w;
-  mark(0, (hipStream_t)stream);
+  mark(0, stream);
   rc = launch_route(x, wt->router_w, wt->router_prep, wt->router_bias, gated ? wt->sh_gate_w : nullptr, T, H, E, k,
-                    valid, idx, rw, b.gamma, b.route, (hipStream_t)stream);
+                    valid, idx, rw, b.gamma, b.route, stream);
   if (rc) return rc;
   return run_experts<int>(x, idx, rw, wt->gate_up_q, wt->gate_up_s, wt->down_q, wt->down_s, wt->sh_gate_up_q,
                           wt->sh_gate_up_s, wt->sh_down_q, wt->sh_down_s, gated ? b.gamma : nullptr, T, H, I, I_s, E, k,
-                          out, b.experts, (hipStream_t)stream, 0, nullptr, nullptr, valid);
+                          out, b.experts, stream, 0, nullptr, nullptr, valid, serve);
+}
+}  // namespace
+
+extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt, const uint16_t* x,
+                                              const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                              float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream) {
+  return block_forward(wt, x, valid, T, out, topk_idx, topk_w, ws, ws_bytes, (hipStream_t)stream, nullptr);
+}
+
+extern "C" int janus_moe_block_forward_serve(const janus_moe_block_weights* wt, const uint16_t* x,
+                                             const uint16_t* h_attn, const uint16_t* post_norm_w, float post_eps,
+                                             const uint16_t* next_norm_w, float next_eps, const uint8_t* valid,
+                                             const uint8_t* next_valid, int T, uint16_t* x_out, uint16_t* h_out,
+                                             int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes,
+                                             janus_stream_t stream) {
+  JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward_serve: null weights");
+  int rc = check_norm_sizes(T, wt->H);
+  if (rc) return rc;
+  JANUS_REQUIRE(post_eps >= 0.f && next_eps >= 0.f, JANUS_MOE_EINVAL, "janus_moe_block_forward_serve: negative eps");
+  if (T == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(x && post_norm_w && next_norm_w && x_out && h_out, JANUS_MOE_EINVAL,
+                "janus_moe_block_forward_serve: null pointer");
+  JANUS_REQUIRE(h_out != x && h_out != x_out, JANUS_MOE_EINVAL,
+                "janus_moe_block_forward_serve: h_out must not alias x or x_out");
+  const hipStream_t s = (hipStream_t)stream;
+  // x_out = x + h_attn, h_out = the post-attention norm of it: the MoE's input
+  rc = launch_add_rmsnorm(x, h_attn, post_norm_w, post_eps, nullptr, T, wt->H, x_out, h_out, s);
+  if (rc) return rc;
+  const ServeEpilogue serve = {x_out, next_norm_w, next_eps, next_valid, h_out};
+  return block_forward(wt, h_out, valid, T, nullptr, topk_idx, topk_w, ws, ws_bytes, s, &serve);
 }
 
 extern "C" int janus_moe_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out,

@@ -272,15 +272,19 @@ def _(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, dow
 
 # ---- whole block ---------------------------------------------------------------------------------------------
 
-@torch.library.custom_op("janus_moe::block_forward", mutates_args=())
-def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias: Optional[Tensor], gate_up_q: Tensor,
-                  gate_up_s: Tensor, down_q: Tensor, down_s: Tensor, sh_gate_up_q: Optional[Tensor],
-                  sh_gate_up_s: Optional[Tensor], sh_down_q: Optional[Tensor], sh_down_s: Optional[Tensor],
-                  sh_gate_w: Optional[Tensor], top_k: int,
-                  valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
-    """Router + routed experts + gated shared expert, one fp32 sum rounded once: (out [T, H] bf16, indices [T, k]
-    int32, weights [T, k] fp32). valid: optional [T] bool (or uint8), False = a padding token: routed to no expert
-    (index E, weight 0) and given a zero output row; the other rows are the unmasked result bit for bit."""
+def _check_mask(mask: Optional[Tensor], name: str, T: int, dev: torch.device):
+    if mask is None:
+        return
+    if mask.dtype not in (torch.bool, torch.uint8) or tuple(mask.shape) != (T,) or not mask.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous bool or uint8 [{T}] tensor, got {mask.dtype} "
+                         f"{tuple(mask.shape)}")
+    if mask.device != dev:
+        raise ValueError(f"{name} is on {mask.device}, x on {dev}")
+
+
+def _block_setup(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s, sh_gate_up_q,
+                 sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w, top_k):
+    """Shape and dtype checks of the block's tensors, the janus_moe_block_weights struct over them and a workspace."""
     dev = _require_gpu(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s, sh_gate_up_q,
                        sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w)
     T, H = x.shape
@@ -295,12 +299,6 @@ def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias:
     _expect(down_s, "down_s", torch.bfloat16, (E, H, I // 128))
     if router_bias is not None:
         _expect(router_bias, "router_bias", torch.float32, (E,))
-    if valid is not None:
-        if valid.dtype not in (torch.bool, torch.uint8) or tuple(valid.shape) != (T,) or not valid.is_contiguous():
-            raise ValueError(f"valid: expected a contiguous bool or uint8 [{T}] tensor, got {valid.dtype} "
-                             f"{tuple(valid.shape)}")
-        if valid.device != dev:
-            raise ValueError(f"valid is on {valid.device}, x on {dev}")
     I_s = 0
     if sh_gate_up_q is not None:
         I_s = sh_gate_up_q.shape[0] // 2
@@ -310,18 +308,32 @@ def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias:
         _expect(sh_down_s, "sh_down_s", torch.bfloat16, (H, I_s // 128))
         if sh_gate_w is not None:
             _expect(sh_gate_w, "sh_gate_w", torch.bfloat16, (H,))
-    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
-    rw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     weights = _lib.BlockWeights(H, I, E, top_k, I_s, *[_ptr(t) for t in (
         router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s,
         sh_gate_up_q, sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w)])
-    L = _lib.lib()
-    n = L.janus_moe_block_workspace_bytes(T, H, I, E, top_k, I_s)
-    ws = _workspace(n, dev)
+    ws = _workspace(_lib.lib().janus_moe_block_workspace_bytes(T, H, I, E, top_k, I_s), dev)
+    return dev, T, H, weights, ws
+
+
+@torch.library.custom_op("janus_moe::block_forward", mutates_args=())
+def block_forward(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias: Optional[Tensor], gate_up_q: Tensor,
+                  gate_up_s: Tensor, down_q: Tensor, down_s: Tensor, sh_gate_up_q: Optional[Tensor],
+                  sh_gate_up_s: Optional[Tensor], sh_down_q: Optional[Tensor], sh_down_s: Optional[Tensor],
+                  sh_gate_w: Optional[Tensor], top_k: int,
+                  valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
+    """Router + routed experts + gated shared expert, one fp32 sum rounded once: (out [T, H] bf16, indices [T, k]
+    int32, weights [T, k] fp32). valid: optional [T] bool (or uint8), False = a padding token: routed to no expert
+    (index E, weight 0) and given a zero output row; the other rows are the unmasked result bit for bit."""
+    dev, T, H, weights, ws = _block_setup(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s,
+                                          sh_gate_up_q, sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w, top_k)
+    _check_mask(valid, "valid", T, dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    rw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
-        check(L.janus_moe_block_forward_masked(ctypes.byref(weights), _ptr(x), _ptr(valid), T, _ptr(out), _ptr(idx),
-                                               _ptr(rw), _ptr(ws), ws.numel(), _stream(dev)), "janus_moe_block_forward")
+        check(_lib.lib().janus_moe_block_forward_masked(ctypes.byref(weights), _ptr(x), _ptr(valid), T, _ptr(out),
+                                                        _ptr(idx), _ptr(rw), _ptr(ws), ws.numel(), _stream(dev)),
+              "janus_moe_block_forward")
     return out, idx, rw
 
 
@@ -330,3 +342,66 @@ def _(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_
       sh_down_q, sh_down_s, sh_gate_w, top_k, valid=None):
     T = x.shape[0]
     return (torch.empty_like(x), x.new_empty(T, top_k, dtype=torch.int32), x.new_empty(T, top_k, dtype=torch.float32))
+
+
+@torch.library.custom_op("janus_moe::block_forward_serve", mutates_args=())
+def block_forward_serve(x: Tensor, h_attn: Optional[Tensor], post_norm_w: Tensor, post_eps: float,
+                        next_norm_w: Tensor, next_eps: float, router_w: Tensor, router_prep: Tensor,
+                        router_bias: Optional[Tensor], gate_up_q: Tensor, gate_up_s: Tensor, down_q: Tensor,
+                        down_s: Tensor, sh_gate_up_q: Optional[Tensor], sh_gate_up_s: Optional[Tensor],
+                        sh_down_q: Optional[Tensor], sh_down_s: Optional[Tensor], sh_gate_w: Optional[Tensor],
+                        top_k: int, valid: Optional[Tensor] = None,
+                        next_valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+    """The MoE layer between its serving neighbours (janus/hybrid.py:1096-1105): x1, n1 = _add_norm(x, h_attn,
+    post norm); moe = block(n1) (padding tokens skipped where valid is False); returns _add_norm(x1, moe, next norm,
+    next_valid) = (x_out [T, H], h_out [T, H]), bf16. The combine kernel writes the second _add_norm directly."""
+    dev, T, H, weights, ws = _block_setup(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_s,
+                                          sh_gate_up_q, sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w, top_k)
+    if h_attn is not None:
+        _expect(h_attn, "h_attn", torch.bfloat16, (T, H))
+    _expect(post_norm_w, "post_norm_w", torch.bfloat16, (H,))
+    _expect(next_norm_w, "next_norm_w", torch.bfloat16, (H,))
+    _check_mask(valid, "valid", T, dev)
+    _check_mask(next_valid, "next_valid", T, dev)
+    x_out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    h_out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().janus_moe_block_forward_serve(
+            ctypes.byref(weights), _ptr(x), _ptr(h_attn), _ptr(post_norm_w), float(post_eps), _ptr(next_norm_w),
+            float(next_eps), _ptr(valid), _ptr(next_valid), T, _ptr(x_out), _ptr(h_out), None, None, _ptr(ws),
+            ws.numel(), _stream(dev)), "janus_moe_block_forward_serve")
+    return x_out, h_out
+
+
+@block_forward_serve.register_fake
+def _(x, h_attn, post_norm_w, post_eps, next_norm_w, next_eps, router_w, router_prep, router_bias, gate_up_q,
+      gate_up_s, down_q, down_s, sh_gate_up_q, sh_gate_up_s, sh_down_q, sh_down_s, sh_gate_w, top_k, valid=None,
+      next_valid=None):
+    return torch.empty_like(x), torch.empty_like(x)
+
+
+# ---- neighbours --------------------------------------------------------------------------------------------------
+
+@torch.library.custom_op("janus_moe::add_rmsnorm", mutates_args=())
+def add_rmsnorm(residual: Tensor, h: Optional[Tensor], weight: Tensor, eps: float,
+                valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+    """_add_norm (janus/hybrid.py:267-273): (residual + h in bf16, its Qwen3_5RMSNorm with `weight`, zeroed where valid
+    is False). residual, h [T, H] bf16 (h None: no add), weight [H] bf16."""
+    dev = _require_gpu(residual, h, weight)
+    T, H = residual.shape
+    _expect(residual, "residual", torch.bfloat16, (T, H))
+    if h is not None:
+        _expect(h, "h", torch.bfloat16, (T, H))
+    _expect(weight, "weight", torch.bfloat16, (H,))
+    _check_mask(valid, "valid", T, dev)
+    x_out = torch.empty_like(residual)
+    n_out = torch.empty_like(residual)
+    with torch.cuda.device(dev):
+        check(_lib.lib().janus_moe_add_rmsnorm(_ptr(residual), _ptr(h), _ptr(weight), float(eps), _ptr(valid), T, H,
+                                               _ptr(x_out), _ptr(n_out), _stream(dev)), "janus_moe_add_rmsnorm")
+    return x_out, n_out
+
+
+@add_rmsnorm.register_fake
+def _(residual, h, weight, eps, valid=None):
+    return torch.empty_like(residual), torch.empty_like(residual)

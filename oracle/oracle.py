@@ -14,6 +14,8 @@ A numpy restatement of the reference's algorithm on the int4 group-128 codec, wi
             y = h . W_down (fp64); routed = sum_j w_j y_j (janus/hybrid.py:574-598 semantics).
   block     out = RNE_bf16(routed + sigmoid(x . w_sg) * shared) with one rounding (the shared expert and gate of
             modeling_qwen3_5_moe.py:787-798, kept in fp64 until the output).
+  add_norm  the serving neighbours (janus/hybrid.py:250-273): x = RNE_bf16(residual + h), exact sum, one rounding;
+            n = RNE_bf16(x / sqrt(mean(x^2) + eps) * (1 + w)) in fp64, 0 at masked rows.
 
 fp64 accumulation stands in for "fp32 accumulation in some order": it is closer to the exact value than any fp32
 order, so a kernel's distance to it measures the kernel's own error.
@@ -298,3 +300,20 @@ def bf16_values(t) -> np.ndarray:
     import torch
 
     return bf16_from_bits(t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+# ---- serving neighbours (janus/hybrid.py:250-273) ----------------------------------------------------------------
+
+def add_rmsnorm(residual, h, weight, eps: float, valid=None):
+    """_add_norm: (x, n) with x = RNE_bf16(residual + h) (h None: residual; the sum of two bf16 values is exact in
+    fp64, so one rounding, as torch's bf16 add of an exact fp32 sum) and n = RNE_bf16(x * (mean(x^2) + eps)^-1/2 *
+    (1 + weight)) (Qwen3_5RMSNorm, _rmsnorm :250-254) computed in fp64, rows where valid is False zeroed. Arrays of
+    bf16 values as fp64, rows along the first axis."""
+    x = np.asarray(residual, dtype=np.float64)
+    if h is not None:
+        x = bf16_round(x + np.asarray(h, dtype=np.float64))
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    n = bf16_round(x * r * (1.0 + np.asarray(weight, dtype=np.float64)))
+    if valid is not None:
+        n = np.where(np.asarray(valid, dtype=bool)[..., None], n, 0.0)
+    return x, n

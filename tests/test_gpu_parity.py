@@ -453,3 +453,67 @@ def test_fused_moe_nvfp4_graph_replay(gpu):
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(replayed, eager)
+
+
+# ---- serving neighbours (janus/hybrid.py:250-273, 1096-1105) --------------------------------------------------
+
+@pytest.mark.parametrize("H,with_h,masked", [(256, True, False), (1000, True, True), (2048, False, True),
+                                             (2048, True, True), (4096, True, False)])
+def test_add_rmsnorm_matches_oracle(gpu, H, with_h, masked):
+    """_add_norm on the GPU: the residual add bit for bit, the norm within one bf16 step of the fp64 oracle (almost
+    always equal), masked rows zero. H = 1000 leaves a partial group of four-column lanes."""
+    g = torch.Generator().manual_seed(H)
+    T, eps = 77, 1e-6
+    r = torch.randn(T, H, generator=g).bfloat16()
+    h = (torch.randn(T, H, generator=g) * 2).bfloat16() if with_h else None
+    w = (torch.randn(H, generator=g) * 0.1).bfloat16()
+    valid = torch.arange(T) % 7 != 2 if masked else None
+    x, n = ops.add_rmsnorm(r.to(gpu), None if h is None else h.to(gpu), w.to(gpu), eps,
+                           None if valid is None else valid.to(gpu))
+    ox, on = O.add_rmsnorm(bf16_np(r), None if h is None else bf16_np(h), bf16_np(w), eps,
+                           None if valid is None else valid.numpy())
+    assert np.array_equal(bf16_np(x), ox)
+    got = bf16_np(n)
+    diff = np.abs(got - on)
+    assert np.all(diff <= np.abs(on) * 2.0 ** -7 + 1e-30), diff.max()
+    assert (diff > 0).mean() < 0.01
+    if valid is not None:
+        assert not got[~valid.numpy()].any()
+
+
+def _rmsnorms(H, gpu, seed):
+    M = pytest.importorskip("transformers.models.qwen3_5_moe.modeling_qwen3_5_moe")
+    g = torch.Generator().manual_seed(seed)
+    norms = []
+    for _ in range(2):
+        norm = M.Qwen3_5MoeRMSNorm(H, eps=1e-6)
+        with torch.no_grad():
+            norm.weight.copy_((torch.randn(H, generator=g) * 0.1).bfloat16().float())
+        norms.append(norm.to(gpu).bfloat16())
+    return norms
+
+
+@pytest.mark.parametrize("name,rows", [("tiny", None), ("short", 4), ("headline", 8)])
+def test_block_serve_equals_the_unfused_chain(gpu, name, rows):
+    """The MoE layer with its serving neighbours in one call (the combine writes the next _add_norm): bit for bit
+    the chain add_rmsnorm -> block -> add_rmsnorm of the same kernels, and within the layer bar of torch's own chain
+    (transformers' Qwen3_5MoeRMSNorm, torch bf16 adds) around the same block."""
+    cfg = synth.CONFIGS[name]
+    _, blk = _block(cfg, gpu)
+    x = synth.activations(cfg).to(gpu)
+    h_attn = (synth.activations(cfg, seed=18).float() * 0.5).bfloat16().to(gpu)
+    post, nxt = _rmsnorms(cfg.H, gpu, seed=3)
+    valid = None if rows is None else _padding_mask(cfg.T, rows, seed=rows).to(gpu)
+    with torch.no_grad():
+        xo, ho = blk.serve(x, h_attn, post, nxt, valid, valid)
+        x1, n1 = ops.add_rmsnorm(x, h_attn, post.weight, post.eps)
+        moe = blk(n1, valid=valid)
+        x2, h2 = ops.add_rmsnorm(x1, moe, nxt.weight, nxt.eps, valid)
+        assert torch.equal(xo, x2) and torch.equal(ho, h2)
+        rx1 = x + h_attn
+        rx2 = rx1 + blk(post(rx1), valid=valid)
+        rh = nxt(rx2)
+    keep = np.ones(cfg.T, dtype=bool) if valid is None else valid.cpu().numpy()
+    assert_layer_close(bf16_np(xo)[keep], bf16_np(rx2)[keep], f"{name} residual")
+    assert_layer_close(bf16_np(ho)[keep], bf16_np(rh)[keep], f"{name} next norm")
+    assert not bf16_np(ho)[~keep].any()

@@ -465,3 +465,49 @@ def test_nvfp4_cpu_dequantize_matches_oracle_bit_for_bit():
     got = nvfp4_dequantize(torch.from_numpy(packed), torch.from_numpy(sbytes).view(torch.float8_e4m3fn),
                            torch.from_numpy(g)[:, None])
     assert np.array_equal(O.bf16_values(got), O.nvfp4_dequant(packed, sbytes, g))
+
+
+# ---- serving neighbours ------------------------------------------------------------------------------------------
+
+def test_add_rmsnorm_matches_transformers_rmsnorm_and_torch_bf16_add():
+    """The oracle's _add_norm against the installed transformers Qwen3_5MoeRMSNorm (the module the reference's
+    _rmsnorm restates, janus/hybrid.py:250-254) after torch's bf16 add: x bit for bit; n within one bf16 step, and
+    exactly equal on almost every element (torch's fp32 mean and rsqrt against the oracle's fp64)."""
+    M = pytest.importorskip("transformers.models.qwen3_5_moe.modeling_qwen3_5_moe")
+    g = torch.Generator().manual_seed(0)
+    T, H, eps = 64, 512, 1e-6
+    r = torch.randn(T, H, generator=g).bfloat16()
+    h = (torch.randn(T, H, generator=g) * 3).bfloat16()
+    norm = M.Qwen3_5MoeRMSNorm(H, eps=eps)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(H, generator=g) * 0.1)
+    w = norm.weight.detach().bfloat16()
+    with torch.no_grad():
+        norm.weight.copy_(w.float())
+        xt = r + h
+        nt = norm(xt)
+    valid = np.arange(T) % 5 != 3
+    x, n = O.add_rmsnorm(O.bf16_values(r), O.bf16_values(h), O.bf16_values(w), eps, valid)
+    assert np.array_equal(x, O.bf16_values(xt))
+    want = O.bf16_values(nt)
+    assert not n[~valid].any()
+    step = np.abs(want[valid]) * 2.0 ** -7 + 1e-30
+    diff = np.abs(n[valid] - want[valid])
+    assert np.all(diff <= step), diff.max()
+    assert (diff > 0).mean() < 0.01
+
+
+def test_add_rmsnorm_closed_forms():
+    """A constant row c gives (1 + w) c / sqrt(c^2 + eps); scaling a row by a power of two leaves n unchanged when eps
+    is 0; h None is no add."""
+    H = 256
+    w = O.bf16_round(np.linspace(-0.5, 0.5, H))
+    c = np.full((3, H), 0.75)
+    x, n = O.add_rmsnorm(c, None, w, 1e-2)
+    assert np.array_equal(x, c)
+    assert np.array_equal(n, O.bf16_round((1.0 + w) * 0.75 / math.sqrt(0.75 ** 2 + 1e-2) + 0 * c))
+    rng = np.random.default_rng(1)
+    row = O.bf16_round(rng.standard_normal((4, H)))
+    _, n1 = O.add_rmsnorm(row, None, w, 0.0)
+    _, n2 = O.add_rmsnorm(row * 8.0, None, w, 0.0)
+    assert np.array_equal(n1, n2)
