@@ -106,6 +106,13 @@ def test_argument_errors_return_codes_without_a_gpu(L):
     assert L.janus_moe_align(p, 4, 2, 8, 0, p, p, p, p, 1 << 20, None) == 1
     assert L.janus_moe_router_prepare(None, 16, 512, p, 1 << 30, None) == 1
     assert L.janus_moe_block_forward(None, p, 4, p, None, None, p, 1 << 30, None) == 1
+    assert L.janus_moe_add_rmsnorm(p, p, p, 1e-6, None, 4, 8192, p, p, None) == 1
+    assert "H <= 4096" in _err(L)
+    assert L.janus_moe_add_rmsnorm(p, p, p, -1.0, None, 4, 2048, p, p, None) == 1
+    assert L.janus_moe_add_rmsnorm(p, p, None, 1e-6, None, 4, 2048, p, p, None) == 1
+    assert L.janus_moe_block_forward_serve(None, p, p, p, 1e-6, p, 1e-6, None, None, 4, p, p, None, None, p,
+                                           1 << 30, None) == 1
+    assert L.janus_moe_block_forward_masked(None, p, None, 4, p, None, None, p, 1 << 30, None) == 1
     assert L.janus_moe_profile_events(None, 3) == 1
     assert L.janus_moe_profile_events(None, 0) == 0
 
