@@ -7,7 +7,7 @@
 //   router_logits  approximate logits for every (token, expert): bf16 MFMA over a two-plane split of the fp32 weight
 //                  (w = hi + mid + r, |r| <= 2^-16 |w|), fp32 accumulation, split over k in 512-wide slices.
 //   router_select  one wave per token: the candidate set {e : approx_e >= approx_(k) - 2 delta_t} provably contains the
-//                  top_k, where delta_t >= |approx - exact| (Cauchy-Schwarz on the split residual plus a 2^-15 relative
+//                  top_k, where delta_t >= |approx - exact| (Cauchy-Schwarz on the split residual plus a 2^-17 relative
 //                  allowance for fp32 accumulation). Only candidates in a cluster of approximate values closer than
 //                  2 delta that reaches into the top_k need their exact logit: an fp64 dot product whose error bound
 //                  decides the fp32 rounding, or, within that bound of a rounding midpoint, a double-double sum.
@@ -117,11 +117,13 @@ __global__ void __launch_bounds__(256) router_meta_kernel(int E, RouterPrep p) {
 // the k slice blockIdx.z. The slice of the 64 x rows sits in LDS (shared by the 4 waves); each wave streams its 16
 // expert rows of both planes from global memory, kAhead k-steps ahead.
 //
-// Rounding. Every bf16 x bf16 product is exact in fp32. Each k-step of 32 forms a fresh block sum of 64 products
-// (hi plane, then mid plane, chained in two MFMAs from zero) that VALU adds to the running fp32 sum, so any product
-// passes through at most 32 + 33 roundings in its block, 16 block additions and up to 8 slice additions (in
-// router_select): 89 roundings of at most 2^-23 relative each (truncating arithmetic assumed), well inside the 2^-15
-// allowance the selection uses.
+// Rounding. Every bf16 x bf16 product is exact in fp32. Each k-step of 32 forms a fresh block sum of the 32 hi-plane
+// products (one MFMA from zero) that VALU adds to the running fp32 hi sum; the mid plane (|mid| <= 2^-9 |w|)
+// accumulates in its own MFMA chain over the slice, and the slice's partial is hi sum + mid sum. A hi product passes
+// through at most 31 roundings in its block, 16 block additions, the final addition and up to 8 slice additions (in
+// router_select): 56 roundings of at most 2^-23 relative each (truncating arithmetic assumed), 2^-17.2 of sum |x w|;
+// a mid product through at most 512 + 1 + 8, which is 521 * 2^-23 * 2^-9 < 2^-22 of sum |x w|. Together within the
+// 2^-17 allowance the selection uses, with sum |x w| <= ||x|| ||w||.
 constexpr int kSteps = kSlice / 32;  // k-steps per slice
 constexpr int kAhead = 8;            // weight fragment loads in flight per wave
 constexpr int kTileT = 64;           // tokens per workgroup
@@ -160,9 +162,9 @@ __global__ void __launch_bounds__(256, 2) router_logits_kernel(const uint16_t* _
   for (int s = 0; s < kAhead; ++s) load_w(s, s);
   __syncthreads();
 
-  f32x4 acc[4];
+  f32x4 acc[4], accm[4];  // hi-plane running sums (fresh block per step), mid-plane MFMA chains
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int tb = 0; tb < 4; ++tb) acc[tb] = accm[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
@@ -174,8 +176,8 @@ __global__ void __launch_bounds__(256, 2) router_logits_kernel(const uint16_t* _
     for (int tb = 0; tb < 4; ++tb) {
       const int row = 16 * tb + nl;
       const bf16x8 xf = *reinterpret_cast<const bf16x8*>(xs + row * kXRowBytes + (((4 * s + g) ^ nl) * 16));
-      f32x4 b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hf, xf, zero4, 0, 0, 0);
-      b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, xf, b, 0, 0, 0);
+      const f32x4 b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hf, xf, zero4, 0, 0, 0);
+      accm[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, xf, accm[tb], 0, 0, 0);
       acc[tb] += b;
       asm volatile("" : "+v"(acc[tb]));  // add now: left alone, the compiler keeps every step's block sum live
     }
@@ -187,7 +189,8 @@ __global__ void __launch_bounds__(256, 2) router_logits_kernel(const uint16_t* _
     const int t = t0 + tb * 16 + nl;
     if (t < T)
       *reinterpret_cast<float4*>(partial + ((long)blockIdx.z * T + t) * Epad + ebase) =
-          make_float4(acc[tb][0], acc[tb][1], acc[tb][2], acc[tb][3]);
+          make_float4(acc[tb][0] + accm[tb][0], acc[tb][1] + accm[tb][1], acc[tb][2] + accm[tb][2],
+                      acc[tb][3] + accm[tb][3]);
   }
 }
 
@@ -433,7 +436,7 @@ __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
     if (lane == 0 && gamma) gamma[t] = 1.0f / (1.0f + __expf(-gdot));
   }
   const double xnorm = sqrt((double)ss) * (1.0 + 1e-5);
-  const double delta = xnorm * (p.meta[0] + 0x1p-15 * p.meta[1]) + 1e-30;
+  const double delta = xnorm * (p.meta[0] + 0x1p-17 * p.meta[1]) + 1e-30;
 
   // k-th largest approximate value: binary search on the order-preserving keys, counting with ballots
   uint32_t key[NJ];
