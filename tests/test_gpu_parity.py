@@ -189,7 +189,7 @@ def _block(cfg, gpu, seed=17):
     return L, blk
 
 
-@pytest.mark.parametrize("name,sample", [("tiny", None), ("short", None), ("headline", 48), ("zipf", 48)])
+@pytest.mark.parametrize("name,sample", [("tiny", None), ("short", None), ("headline", 48), ("zipf", 48), ("max", 32)])
 def test_block_matches_oracle(gpu, name, sample):
     cfg = synth.CONFIGS[name]
     L, blk = _block(cfg, gpu)
