@@ -14,7 +14,8 @@ known size. With JANUS_MOE_SCHEDULE=split in the environment the GEMMs run as on
 the stages then also report gate_up and down, and the traffic entry is null. The same layer replayed
 from a HIP graph is timed afterwards and reported as graph_tokens_per_s. The CPU baseline is the reference's CPU
 algorithm (dequantise-per-call + padded bmm, oracle/cpu_bmm.py) on the same inputs, on all host cores, on a bounded
-sample. Prints one JSON line.
+sample. `variants_us` times the paths beside the headline one on the same inputs (right-padding mask, the serving
+sequence fused and unfused, NVFP4 stacks). Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -91,6 +92,88 @@ def make_layer(name: str, dev: torch.device):
     x = synth.activations(cfg).to(dev)
     blk = W4A16SparseMoeBlock.from_tensors(layer, cfg.k).to(dev)
     return cfg, layer, x, blk
+
+
+# ---- the paths beside the headline one -------------------------------------------------------------------------
+
+def _time_us(fn, iters: int = 20) -> float:
+    """Average device time of fn() over `iters` eager calls after 3 warm-ups, HIP events on the current stream."""
+    for _ in range(3):
+        fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / iters
+
+
+class _Norm(torch.nn.Module):
+    """A Qwen3_5RMSNorm's two attributes (weight, eps), for the serving sequence."""
+
+    def __init__(self, weight, eps=1e-6):
+        super().__init__()
+        self.weight, self.eps = weight, eps
+
+
+def variant_timings(cfg, x, blk, dev) -> dict:
+    """Device time per call (us) of the paths beside the headline layer, on the same inputs:
+      - masked_25pct: the layer with a level batch's right padding (8 rows, a quarter of the positions padding);
+      - serve_unfused / serve_fused: _add_norm, the layer and the next _add_norm as three calls, and as one call whose
+        combine writes the second _add_norm;
+      - experts_int4 / experts_nvfp4: fused_moe on the layer's routing with the int4 stacks and with NVFP4 stacks of
+        the same shape (random weights quantised on the GPU).
+    Each entry that fails is reported as its error text instead."""
+    from janus_amd import ops
+    from janus_amd.hybrid import nvfp4_quantize
+    from janus_amd.moe_w4a16 import fused_moe
+
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(5)
+
+    def run(name, fn):
+        try:
+            with torch.no_grad():
+                out[name] = _time_us(fn)
+        except Exception as exc:  # an extra line of evidence must not take the headline measurement with it
+            out[name] = f"{type(exc).__name__}: {exc}"[:200]
+
+    rows = 8
+    length = cfg.T // rows
+    lengths = torch.full((rows,), length, device=dev)
+    lengths[::2] = length // 2                       # half the rows half full: a quarter of the positions padding
+    valid = (torch.arange(length, device=dev)[None] < lengths[:, None]).reshape(-1)
+    run("masked_25pct", lambda: blk(x, valid=valid))
+
+    h_attn = (torch.randn(x.shape, generator=g, device=dev) * 0.5).bfloat16()
+    post = _Norm((torch.randn(cfg.H, generator=g, device=dev) * 0.1).bfloat16())
+    nxt = _Norm((torch.randn(cfg.H, generator=g, device=dev) * 0.1).bfloat16())
+
+    def unfused():
+        x1, n1 = ops.add_rmsnorm(x, h_attn, post.weight, post.eps)
+        return ops.add_rmsnorm(x1, blk(n1), nxt.weight, nxt.eps)
+
+    run("serve_unfused", unfused)
+    run("serve_fused", lambda: blk.serve(x, h_attn, post, nxt))
+
+    with torch.no_grad():
+        _, w, idx = blk.gate(x)
+    ex = blk.experts
+    run("experts_int4", lambda: fused_moe(x, idx, w, ex.gate_up, ex.gate_up_scale, None, ex.down, ex.down_scale, None))
+    try:
+        def stack(rows_, k):
+            parts = [nvfp4_quantize(torch.randn(rows_, k, generator=g, device=dev) * 0.05) for _ in range(cfg.E)]
+            return (torch.stack([p[0] for p in parts]), torch.stack([p[1] for p in parts]),
+                    torch.stack([p[2] for p in parts])[:, None, None].expand(cfg.E, rows_, 1).contiguous())
+        gu, gus, gug = stack(2 * cfg.I, cfg.H)
+        dn, dns, dng = stack(cfg.H, cfg.I)
+        run("experts_nvfp4", lambda: fused_moe(x, idx, w, gu, gus, gug, dn, dns, dng))
+        del gu, gus, gug, dn, dns, dng
+    except Exception as exc:
+        out["experts_nvfp4"] = f"{type(exc).__name__}: {exc}"[:200]
+    return out
 
 
 # ---- counters (child runs under rocprofv3) ---------------------------------------------------------------------
@@ -272,6 +355,7 @@ def main() -> int:
         "stages_us": stage_us,
         "graph_tokens_per_s": cfg.T / graph_s, "graph_ms_per_step": graph_s * 1e3,
     }
+    result["variants_us"] = variant_timings(cfg, x, blk, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layer, x, cfg.k)
     print(json.dumps(result))
