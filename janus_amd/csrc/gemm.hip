@@ -217,7 +217,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   const bool active = col0 < out_cols;
   const int nrb = (rows + 15) / 16;
 
-  // ---- activation rows this lane stages: round r covers rows 16r..16r+15, this wave rows 16r + 4w + (lane >> 4), 16
+  // ---- activation rows this lane stages: pass r covers rows 16r..16r+15, this wave rows 16r + 4w + (lane >> 4), 16
   // lanes per row each taking one 16-byte chunk (chunk lane & 15) ----
   // 32-bit byte offsets from wave-uniform bases (SGPR base + VGPR offset addressing) keep the pointer state small.
   const unsigned char* abase;
@@ -237,7 +237,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       arow = pos0 + rr;
     aoff[r] = (uint32_t)arow * (uint32_t)(K * 2) + (lane & 15) * 16;
   }
-  const int arow0 = 4 * wave + (lane >> 4);  // this lane's row in round 0
+  const int arow0 = 4 * wave + (lane >> 4);  // this lane's row in pass 0
 
   // ---- weight rows of this lane, one per column block (an idle wave reads row 0 and discards it) ----
   const unsigned char* wbase = reinterpret_cast<const unsigned char*>(wq);

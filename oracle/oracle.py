@@ -1,5 +1,5 @@
 """CPU oracle of the W4A16 MoE layer. TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py as the checker; the product (janus_amd) never imports it.
+cpu_baseline leg of bench.py to check results against; the product (janus_amd) never imports it.
 
 A numpy restatement of the reference's algorithm on the int4 group-128 codec, with every rounding point explicit:
 
