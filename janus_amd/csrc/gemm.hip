@@ -586,6 +586,8 @@ DeviceShape device_shape() {
 int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* sched, hipStream_t stream) {
   const char* env = getenv("JANUS_MOE_SCHEDULE");
   if (env && strcmp(env, "split") == 0) return kNotFused;
+  // a CU mask can leave an XCD without workgroups, and its queue would never drain
+  if (getenv("HSA_CU_MASK") || getenv("ROC_GLOBAL_CU_MASK")) return kNotFused;
   GemmParams gu = gu_in, dn = dn_in;
   if (gu.n_shared_chunks + gu.max_chunks == 0) return kNotFused;
   if (gu.n_shared_chunks && (gu.K_sh != gu.K || dn.K_sh != dn.K)) return kNotFused;
