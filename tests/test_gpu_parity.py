@@ -309,6 +309,24 @@ def test_persistent_schedule_equals_one_launch_per_gemm(gpu, name, monkeypatch):
             assert torch.equal(out, split)
 
 
+def test_persistent_schedule_over_token_counts(gpu, monkeypatch):
+    """Token counts around the 96-row chunk and the per-XCD queue boundaries (few chunks: empty queues; shared chunks
+    of one token), each call equal to one launch per GEMM bit for bit."""
+    cfg = synth.CONFIGS["short"]
+    _, blk = _block(cfg, gpu)
+    full = synth.activations(synth.LayerConfig("sweep", T=1000, H=cfg.H, E=cfg.E, k=cfg.k, I=cfg.I, I_s=cfg.I_s))
+    full = full.to(gpu)
+    with torch.no_grad():
+        for T in (1, 2, 7, 95, 96, 97, 191, 193, 385, 769, 1000):
+            x = full[:T].contiguous()
+            monkeypatch.setenv("JANUS_MOE_SCHEDULE", "split")
+            split = blk(x).clone()
+            monkeypatch.delenv("JANUS_MOE_SCHEDULE")
+            out = blk(x)
+            torch.cuda.synchronize()
+            assert torch.equal(out, split), T
+
+
 @pytest.mark.parametrize("S", [1, 3, 700])
 def test_persistent_schedule_fused_moe_int4_and_nvfp4(gpu, S, monkeypatch):
     """fused_moe on both codecs, one token (most XCD queues empty) to several chunks per expert: the persistent launch
