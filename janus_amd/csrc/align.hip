@@ -1,8 +1,10 @@
 // Token-to-expert sort / align / permute on gfx950: a bit-exact integer restatement of align()
 // (janus/moe_w4a16.py:89-106). The stable order is the assignment id order, exactly as torch.argsort(stable=True) in
-// the reference. Two schedules, chosen by size, with the same results:
-//   small (A <= 65536 assignments: every batch up to 8K tokens at top-8): blocks of 256 assignments, two launches
-//     (rank, place), every block recomputing the per-expert prefix it needs from the blocks' histograms;
+// the reference. Three schedules, chosen by size, with the same results:
+//   one launch (A <= 32768 assignments: every batch up to 4K tokens at top-8): blocks of 256 assignments, each
+//     workgroup counting all assignments per expert itself (LDS histograms) and placing its block;
+//   small (A <= 65536): blocks of 256 assignments, two launches (rank, place), every block recomputing the
+//     per-expert prefix it needs from the blocks' histograms;
 //   large: blocks of 1024 assignments, three launches: rank (an LDS histogram and the stable rank of every assignment
 //     among the block's assignments of the same expert, the block's waves taking their turn in order), scan (one
 //     workgroup: per-expert totals, per-(block, expert) offsets, padded starts), scatter.
@@ -208,6 +210,90 @@ __global__ void __launch_bounds__(kPlaceThreads) align_small_place_kernel(
   }
 }
 
+// Up to kOneMaxA assignments the small schedule's two launches are one: every workgroup also counts all A
+// assignments per expert (and those before its block) in LDS, from the expert ids themselves, in place of the
+// per-block histograms the second launch would read. Each workgroup reads all of idx (64 KB at 16K assignments, from
+// the L2), which is what bounds the size. The results are those of the two launches.
+constexpr int kOneMaxA = 32768;
+
+template <typename IdxT, typename OutT>
+__global__ void __launch_bounds__(kPlaceThreads) align_one_kernel(
+    const IdxT* __restrict__ idx, int A, int E, int nbits, int block, OutT* __restrict__ sorted_ids, int sorted_len,
+    OutT* __restrict__ expert_ids, int tiles, OutT* __restrict__ total_out, int4* __restrict__ chunks,
+    int chunk_rows, int* __restrict__ num_chunks, int* __restrict__ clear, int clear_n) {
+  __shared__ int all_c[kMaxExperts], before_c[kMaxExperts];
+  __shared__ int wcnt[kSmallWaves][kMaxExperts];  // per-wave counts of the block, then per-wave offsets
+  __shared__ int cum[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int scan_tmp[16];
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave, b = blockIdx.x;
+  const int a0 = b * kSmallBlock;
+  for (int i = tid; i < kMaxExperts; i += kPlaceThreads) {
+    all_c[i] = 0;
+    before_c[i] = 0;
+  }
+  for (int i = tid; i < kSmallWaves * kMaxExperts; i += kPlaceThreads) (&wcnt[0][0])[i] = 0;
+  // this block's own assignment, loaded together with the first pass below
+  int e = -1;
+  const int a = a0 + tid;
+  if (tid < kSmallBlock && a < A) {
+    const long v = (long)idx[a];
+    e = (v >= 0 && v < E) ? (int)v : -1;
+  }
+  __syncthreads();
+  // every assignment, sixteen loads in flight per thread (one pass up to 16K assignments)
+  constexpr int kLoads = 16;
+  for (int i0 = tid; i0 < A; i0 += kLoads * kPlaceThreads) {
+    long v[kLoads];
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      const int i = i0 + u * kPlaceThreads;
+      v[u] = i < A ? (long)idx[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      if (v[u] >= 0 && v[u] < E) {
+        atomicAdd(&all_c[(int)v[u]], 1);
+        if (i0 + u * kPlaceThreads < a0) atomicAdd(&before_c[(int)v[u]], 1);
+      }
+    }
+  }
+  // stable rank of the block's assignments among the block's assignments of the same expert (as align_small_rank)
+  Peers pr = {0, 0, 0};
+  if (tid < kSmallBlock) {  // whole waves
+    pr = wave_peers(e, nbits);
+    if (e >= 0 && lane == pr.leader) wcnt[wave][e] = pr.count;
+  }
+  __syncthreads();
+  if (tid < E) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < kSmallWaves; ++w) {
+      const int h = wcnt[w][tid];
+      wcnt[w][tid] = c;
+      c += h;
+    }
+  }
+  const int count = tid < E ? all_c[tid] : 0;
+  const int padded = (count + block - 1) / block * block;
+  const int incl = block_inclusive_scan(tid < E ? padded : 0, scan_tmp);  // its barriers order the wcnt offsets too
+  const int start = incl - padded;
+  if (tid < E) {
+    cum[tid] = incl;
+    base[tid] = start + before_c[tid];
+  }
+  __syncthreads();
+  if (e >= 0) sorted_ids[base[e] + wcnt[wave][e] + pr.rank] = (OutT)a;
+  if (b == 0) {
+    if (tid < E)
+      for (int i = count; i < padded; ++i) sorted_ids[start + i] = (OutT)A;
+    const int total = E > 0 ? cum[E - 1] : 0;
+    for (int i = total + tid; i < sorted_len; i += kPlaceThreads) sorted_ids[i] = (OutT)A;
+    write_plan<OutT>(cum, E, block, count, start, expert_ids, tiles, total_out, chunks, chunk_rows, num_chunks,
+                     scan_tmp, clear, clear_n);
+  }
+}
+
 template <typename IdxT, typename OutT>
 __global__ void __launch_bounds__(kRankThreads) align_rank_kernel(const IdxT* __restrict__ idx, int A, int E, int nbits,
                                                                   int* __restrict__ hist, int* __restrict__ local_rank,
@@ -320,6 +406,13 @@ template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
                  int* clear, int clear_n, hipStream_t stream) {
+  if (A <= kOneMaxA) {
+    hipLaunchKernelGGL((align_one_kernel<IdxT, OutT>), dim3(A > 0 ? ceil_div(A, kSmallBlock) : 1), dim3(kPlaceThreads),
+                       0, stream, idx, A, E, expert_bits(E), block, sorted_ids, sorted_len, expert_ids, tiles, total,
+                       chunks, chunk_rows, num_chunks, clear, clear_n);
+    JANUS_LAUNCH_CHECK("align_one");
+    return JANUS_MOE_OK;
+  }
   if (A <= kSmallMaxA) {
     const int nb = ceil_div(A, kSmallBlock);
     if (nb > 0) {

@@ -63,7 +63,8 @@ def test_dequant_bit_exact_over_codes_and_scales(gpu):
     (0, 2, 8, 16, 0), (1, 1, 1, 16, 0), (5, 2, 8, 16, 0), (40, 2, 8, 16, 1), (96, 8, 256, 16, 0),
     (700, 8, 16, 64, 1), (2048, 8, 256, 64, 0), (2048, 8, 256, 16, 2), (3000, 4, 60, 32, 0),
     (16384, 8, 256, 64, 0), (16384, 8, 256, 128, 2), (1000, 8, 1024, 16, 0),
-    # either side of the small schedule's limit (65536 assignments)
+    # either side of the one-launch limit (32768 assignments) and of the small schedule's (65536)
+    (4096, 8, 256, 16, 2), (4097, 8, 256, 16, 0), (32768, 1, 1024, 64, 1),
     (8191, 8, 256, 16, 1), (8192, 8, 64, 16, 2), (65537, 1, 1024, 16, 2),
 ])
 def test_align_bit_exact(gpu, S, k, E, block, skew):
