@@ -19,8 +19,19 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as
 
 // The normalisation of a row held as fp32 values of its bf16 x (v[j][0..3] = columns 4 (lane + 64 j) .. +3), written
 // as bf16 to n_row. ncol4 = H / 4.
+// The lane's norm weights (columns 4 (lane + 64 j) .. +3), loaded before the row's other reads are used.
 template <int NV>
-__device__ __forceinline__ void rmsnorm_row(const float (&v)[NV][4], int H, int ncol4, const uint16_t* __restrict__ w,
+__device__ __forceinline__ void load_norm_weights(const uint16_t* __restrict__ w, int ncol4, uint2 (&wb)[NV]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c4 = lane + kWave * j;
+    wb[j] = c4 < ncol4 ? *reinterpret_cast<const uint2*>(w + 4 * c4) : make_uint2(0u, 0u);
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void rmsnorm_row(const float (&v)[NV][4], int H, int ncol4, const uint2 (&wbs)[NV],
                                             float eps, bool keep, uint16_t* n_row) {
   const int lane = threadIdx.x & (kWave - 1);
   float ss = 0.f;
@@ -35,7 +46,7 @@ __device__ __forceinline__ void rmsnorm_row(const float (&v)[NV][4], int H, int 
   for (int j = 0; j < NV; ++j) {
     const int c4 = lane + kWave * j;
     if (c4 >= ncol4) continue;
-    const uint2 wb = *reinterpret_cast<const uint2*>(w + 4 * c4);
+    const uint2 wb = wbs[j];
     const float wv[4] = {bf16_to_f32(wb.x & 0xFFFFu), bf16_to_f32(wb.x >> 16), bf16_to_f32(wb.y & 0xFFFFu),
                          bf16_to_f32(wb.y >> 16)};
     float o[4];
@@ -53,6 +64,8 @@ __global__ void __launch_bounds__(kNormWaves * kWave) add_rmsnorm_kernel(
   const long t = (long)blockIdx.x * kNormWaves + threadIdx.x / kWave;
   if (t >= T) return;  // whole waves; no barriers
   const int ncol4 = H / 4;
+  uint2 wb[NV];
+  load_norm_weights<NV>(w, ncol4, wb);
   float v[NV][4];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -77,12 +90,14 @@ __global__ void __launch_bounds__(kNormWaves * kWave) add_rmsnorm_kernel(
     v[j][3] = bf16_to_f32(xb.y >> 16);
     if (x_out) *reinterpret_cast<uint2*>(x_out + t * H + 4 * c4) = xb;
   }
-  rmsnorm_row<NV>(v, H, ncol4, w, eps, !valid || valid[t], n_out + t * H);
+  rmsnorm_row<NV>(v, H, ncol4, wb, eps, !valid || valid[t], n_out + t * H);
 }
 
 // The combine with the next residual add and norm: moe = bf16(sum_j slots[t, j]) in slot order (the plain combine's
 // value), x = bf16(x_res + moe) written back over x_res, n = the norm of x. A token the MoE skipped (moe_valid[t] == 0)
-// contributes moe = 0 and its slots are not read.
+// contributes moe = 0 and its slots are not read. The slots are read kSlotBatch at a time for all of the lane's
+// columns, so a row costs ceil(nslots / kSlotBatch) memory round trips (one slot at a time for rows past 2048
+// columns, whose registers would not allow two waves per SIMD otherwise).
 template <int NV>
 __global__ void __launch_bounds__(kNormWaves * kWave) combine_add_rmsnorm_kernel(
     const float4* __restrict__ slots, int nslots, const uint8_t* __restrict__ moe_valid, uint16_t* x_res,
@@ -92,6 +107,44 @@ __global__ void __launch_bounds__(kNormWaves * kWave) combine_add_rmsnorm_kernel
   if (t >= T) return;
   const int ncol4 = H / 4;
   const bool routed = !moe_valid || moe_valid[t];
+  uint2 wb[NV], rb[NV];
+  load_norm_weights<NV>(w, ncol4, wb);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c4 = lane + kWave * j;
+    rb[j] = c4 < ncol4 ? *reinterpret_cast<const uint2*>(x_res + t * H + 4 * c4) : make_uint2(0u, 0u);
+  }
+  constexpr int kSlotBatch = NV <= 8 ? 3 : 1;
+  float4 s[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (routed) {
+    const float4* src = slots + t * nslots * ncol4 + lane;
+    for (int k0 = 0; k0 < nslots; k0 += kSlotBatch) {
+      float4 a[kSlotBatch][NV];
+#pragma unroll
+      for (int kk = 0; kk < kSlotBatch; ++kk)
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+          if (k0 + kk < nslots && lane + kWave * j < ncol4) a[kk][j] = src[(long)(k0 + kk) * ncol4 + kWave * j];
+#pragma unroll
+      for (int kk = 0; kk < kSlotBatch; ++kk) {
+        if (k0 + kk >= nslots) break;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          if (lane + kWave * j >= ncol4) continue;
+          if (k0 + kk == 0) {
+            s[j] = a[kk][j];  // slot 0 starts the sum, as in the plain combine
+          } else {
+            s[j].x += a[kk][j].x;
+            s[j].y += a[kk][j].y;
+            s[j].z += a[kk][j].z;
+            s[j].w += a[kk][j].w;
+          }
+        }
+      }
+    }
+  }
   float v[NV][4];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -99,24 +152,11 @@ __global__ void __launch_bounds__(kNormWaves * kWave) combine_add_rmsnorm_kernel
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[j][i] = 0.f;
     if (c4 >= ncol4) continue;
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (routed) {
-      const float4* src = slots + t * nslots * ncol4 + c4;
-      s = src[0];
-      for (int k = 1; k < nslots; ++k) {
-        const float4 a = src[(long)k * ncol4];
-        s.x += a.x;
-        s.y += a.y;
-        s.z += a.z;
-        s.w += a.w;
-      }
-    }
-    const uint2 mb = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));  // the MoE output, bf16
-    const uint2 rb = *reinterpret_cast<const uint2*>(x_res + t * H + 4 * c4);
-    const float x[4] = {bf16_to_f32(rb.x & 0xFFFFu) + bf16_to_f32(mb.x & 0xFFFFu),
-                        bf16_to_f32(rb.x >> 16) + bf16_to_f32(mb.x >> 16),
-                        bf16_to_f32(rb.y & 0xFFFFu) + bf16_to_f32(mb.y & 0xFFFFu),
-                        bf16_to_f32(rb.y >> 16) + bf16_to_f32(mb.y >> 16)};
+    const uint2 mb = make_uint2(pack_bf16x2(s[j].x, s[j].y), pack_bf16x2(s[j].z, s[j].w));  // the MoE output, bf16
+    const float x[4] = {bf16_to_f32(rb[j].x & 0xFFFFu) + bf16_to_f32(mb.x & 0xFFFFu),
+                        bf16_to_f32(rb[j].x >> 16) + bf16_to_f32(mb.x >> 16),
+                        bf16_to_f32(rb[j].y & 0xFFFFu) + bf16_to_f32(mb.y & 0xFFFFu),
+                        bf16_to_f32(rb[j].y >> 16) + bf16_to_f32(mb.y >> 16)};
     const uint2 xb = make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
     v[j][0] = bf16_to_f32(xb.x & 0xFFFFu);
     v[j][1] = bf16_to_f32(xb.x >> 16);
@@ -124,7 +164,7 @@ __global__ void __launch_bounds__(kNormWaves * kWave) combine_add_rmsnorm_kernel
     v[j][3] = bf16_to_f32(xb.y >> 16);
     *reinterpret_cast<uint2*>(x_res + t * H + 4 * c4) = xb;
   }
-  rmsnorm_row<NV>(v, H, ncol4, w, eps, !valid || valid[t], n_out + t * H);
+  rmsnorm_row<NV>(v, H, ncol4, wb, eps, !valid || valid[t], n_out + t * H);
 }
 
 }  // namespace
