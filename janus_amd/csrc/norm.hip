@@ -64,8 +64,16 @@ __global__ void __launch_bounds__(kNormWaves * kWave) add_rmsnorm_kernel(
   const long t = (long)blockIdx.x * kNormWaves + threadIdx.x / kWave;
   if (t >= T) return;  // whole waves; no barriers
   const int ncol4 = H / 4;
-  uint2 wb[NV];
+  uint2 wb[NV], rbs[NV], hbs[NV];
   load_norm_weights<NV>(w, ncol4, wb);
+  // every load of the row before the first store: the outputs may alias the inputs (an element is read and written by
+  // the same lane only), so the compiler would otherwise wait for each column group's loads in turn
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c4 = lane + kWave * j;
+    rbs[j] = c4 < ncol4 ? *reinterpret_cast<const uint2*>(residual + t * H + 4 * c4) : make_uint2(0u, 0u);
+    hbs[j] = (h && c4 < ncol4) ? *reinterpret_cast<const uint2*>(h + t * H + 4 * c4) : make_uint2(0u, 0u);
+  }
   float v[NV][4];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -73,11 +81,11 @@ __global__ void __launch_bounds__(kNormWaves * kWave) add_rmsnorm_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[j][i] = 0.f;
     if (c4 >= ncol4) continue;
-    const uint2 rb = *reinterpret_cast<const uint2*>(residual + t * H + 4 * c4);
+    const uint2 rb = rbs[j];
     float x[4] = {bf16_to_f32(rb.x & 0xFFFFu), bf16_to_f32(rb.x >> 16), bf16_to_f32(rb.y & 0xFFFFu),
                   bf16_to_f32(rb.y >> 16)};
     if (h) {
-      const uint2 hb = *reinterpret_cast<const uint2*>(h + t * H + 4 * c4);
+      const uint2 hb = hbs[j];
       x[0] += bf16_to_f32(hb.x & 0xFFFFu);
       x[1] += bf16_to_f32(hb.x >> 16);
       x[2] += bf16_to_f32(hb.y & 0xFFFFu);
