@@ -351,27 +351,52 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       }
     }
   } else {
+    // every row's assignment id, then its routing weight, before the first store: as far as the compiler knows the
+    // slots may alias the routing weights, and a load written after a row block's stores would wait for them, one
+    // memory round trip per row block
+    // (rows past the chunk read its first row's: loads without a branch, whose values are not used)
+    int id[kRowBlocks];
+    float wt[kRowBlocks];
+    if (shared) {
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb) {
+        const int m = rb * 16 + nl;
+        id[rb] = pos0 + (m < rows ? m : 0);  // the token
+      }
+      if (p.gamma) {
+#pragma unroll
+        for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = p.gamma[id[rb]];
+      } else {
+#pragma unroll
+        for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = 1.0f;
+      }
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb) {
+        const int m = rb * 16 + nl;
+        id[rb] = p.sorted_ids[pos0 + (m < rows ? m : 0)];
+      }
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = p.route_w[id[rb]];
+    }
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
       const int m = rb * 16 + nl;
       if (rb >= nrb || m >= rows) continue;
       int tok, slot;
-      float wt;
       if (shared) {
-        tok = pos0 + m;
+        tok = id[rb];
         slot = p.topk;
-        wt = p.gamma ? p.gamma[tok] : 1.0f;
       } else {
-        const int id = p.sorted_ids[pos0 + m];
-        tok = id / p.topk;
-        slot = id - tok * p.topk;
-        wt = p.route_w[id];
+        tok = id[rb] / p.topk;
+        slot = id[rb] - tok * p.topk;
       }
       float* orow = p.slots + ((long)tok * p.nslots + slot) * N + col0 + 4 * g;
+      const float w = wt[rb];
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb)
         *reinterpret_cast<float4*>(orow + 16 * cb) =
-            make_float4(wt * acc[rb][cb][0], wt * acc[rb][cb][1], wt * acc[rb][cb][2], wt * acc[rb][cb][3]);
+            make_float4(w * acc[rb][cb][0], w * acc[rb][cb][1], w * acc[rb][cb][2], w * acc[rb][cb][3]);
     }
   }
 }
