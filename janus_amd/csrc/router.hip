@@ -404,17 +404,30 @@ __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
     xv[j] = ok ? *reinterpret_cast<const uint4*>(x + (long)t * H + h0) : make_uint4(0, 0, 0, 0);
     gv[j] = (ok && wsg) ? *reinterpret_cast<const uint4*>(wsg + h0) : make_uint4(0, 0, 0, 0);
   }
+  // The slices' partial sums and the bias, every load issued before the first is used. The loads take no branch:
+  // a slice past nslice re-reads slice 0 and a column past Epad re-reads the lane's column of block 0 (both in
+  // bounds), and the values that do not count are dropped afterwards. A load under a branch, feeding a running sum,
+  // would cost a memory round trip each.
   float av[NJ];
   const float* prow = partial + (long)t * Epad + lane;
   const long zstride = (long)T * Epad;
+  float pz[NJ][NHV], bj[NJ];  // nslice = ceil(H / 512) <= NHV
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int cj = 64 * j < Epad ? 64 * j : 0;  // uniform
+#pragma unroll
+    for (int z = 0; z < NHV; ++z) pz[j][z] = prow[(z < nslice ? z : 0) * zstride + cj];
+    const int e = lane + 64 * j;
+    bj[j] = bias ? bias[e < E ? e : 0] : 0.f;
+  }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const bool ok = lane + 64 * j < E;
     float sj = 0.f;
 #pragma unroll
-    for (int z = 0; z < kMaxHv; ++z)
-      if (z < nslice) sj += ok ? prow[z * zstride + 64 * j] : 0.f;
-    if (bias) sj += ok ? bias[lane + 64 * j] : 0.f;
+    for (int z = 0; z < NHV; ++z)
+      if (z < nslice) sj += ok ? pz[j][z] : 0.f;
+    if (bias) sj += ok ? bj[j] : 0.f;
     av[j] = ok ? sj : -__builtin_inff();
   }
 
