@@ -166,8 +166,11 @@ __global__ void __launch_bounds__(kPlaceThreads) align_small_place_kernel(
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int j = j0 + u * G;
-        h[u] = j < nb ? hist[(long)j * E + x] : 0;
+        h[u] = hist[(long)(j < nb ? j : nb - 1) * E + x];  // no branch: a row past nb re-reads the last, dropped below
       }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (j0 + u * G >= nb) h[u] = 0;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         pc += h[u];
@@ -241,15 +244,19 @@ __global__ void __launch_bounds__(kPlaceThreads) align_one_kernel(
     e = (v >= 0 && v < E) ? (int)v : -1;
   }
   __syncthreads();
-  // every assignment, sixteen loads in flight per thread (one pass up to 16K assignments)
+  // every assignment, sixteen loads in flight per thread (one pass up to 16K assignments). The loads take no branch
+  // (an index past A re-reads the last id, dropped afterwards): a load under a branch would be waited for at once.
   constexpr int kLoads = 16;
   for (int i0 = tid; i0 < A; i0 += kLoads * kPlaceThreads) {
     long v[kLoads];
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       const int i = i0 + u * kPlaceThreads;
-      v[u] = i < A ? (long)idx[i] : -1;
+      v[u] = (long)idx[i < A ? i : A - 1];
     }
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u)
+      if (i0 + u * kPlaceThreads >= A) v[u] = -1;
 #pragma unroll
     for (int u = 0; u < kLoads; ++u) {
       if (v[u] >= 0 && v[u] < E) {
