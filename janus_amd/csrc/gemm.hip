@@ -225,17 +225,26 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     abase = reinterpret_cast<const unsigned char*>(p.a);
   else
     abase = reinterpret_cast<const unsigned char*>(shared ? p.a_sh : p.a);
+  // Padding rows re-read row 0: finite values, results discarded. A routed gate_up unit's rows are tokens looked up
+  // through sorted_ids, all six lookups issued before the first is used (the branch on `shared` stays outside the
+  // loops: a load selected against another value under it would be waited for at once).
   uint32_t aoff[kRowBlocks];
+  if (MODE == kGateUp && !shared) {
+    int id[kRowBlocks];
 #pragma unroll
-  for (int r = 0; r < kRowBlocks; ++r) {
-    const int row = 16 * r + 4 * wave + (lane >> 4);
-    const int rr = row < rows ? row : 0;  // padding rows re-read row 0: finite values, results discarded
-    int arow;
-    if (MODE == kGateUp)
-      arow = shared ? pos0 + rr : p.sorted_ids[pos0 + rr] / p.topk;
-    else
-      arow = pos0 + rr;
-    aoff[r] = (uint32_t)arow * (uint32_t)(K * 2) + (lane & 15) * 16;
+    for (int r = 0; r < kRowBlocks; ++r) {
+      const int row = 16 * r + 4 * wave + (lane >> 4);
+      id[r] = p.sorted_ids[pos0 + (row < rows ? row : 0)];
+    }
+#pragma unroll
+    for (int r = 0; r < kRowBlocks; ++r)
+      aoff[r] = (uint32_t)(id[r] / p.topk) * (uint32_t)(K * 2) + (lane & 15) * 16;
+  } else {
+#pragma unroll
+    for (int r = 0; r < kRowBlocks; ++r) {
+      const int row = 16 * r + 4 * wave + (lane >> 4);
+      aoff[r] = (uint32_t)(pos0 + (row < rows ? row : 0)) * (uint32_t)(K * 2) + (lane & 15) * 16;
+    }
   }
   const int arow0 = 4 * wave + (lane >> 4);  // this lane's row in pass 0
 
