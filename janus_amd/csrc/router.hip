@@ -153,10 +153,13 @@ __global__ void __launch_bounds__(256, 2) router_logits_kernel(const uint16_t* _
   const uint16_t* hrow = p.hi + (long)(e_ok ? e : 0) * H + k0 + 8 * g;
   const uint16_t* mrow = p.mid + (long)(e_ok ? e : 0) * H + k0 + 8 * g;
   u32x4 wh[kAhead], wm[kAhead];
+  // Loads without a branch, so that all of them are in flight together: an expert past E reads expert 0's row (its
+  // column of partial is padding, never selected), a step past the slice re-reads step 0 (the x tile is zero there,
+  // and finite weights times zero add nothing).
   auto load_w = [&](int slot, int step) __attribute__((always_inline)) {
-    const bool ok = e_ok && 32 * step < klen;
-    wh[slot] = ok ? *reinterpret_cast<const u32x4*>(hrow + 32 * step) : u32x4{0, 0, 0, 0};
-    wm[slot] = ok ? *reinterpret_cast<const u32x4*>(mrow + 32 * step) : u32x4{0, 0, 0, 0};
+    const int st = 32 * step < klen ? step : 0;
+    wh[slot] = *reinterpret_cast<const u32x4*>(hrow + 32 * st);
+    wm[slot] = *reinterpret_cast<const u32x4*>(mrow + 32 * st);
   };
 #pragma unroll
   for (int s = 0; s < kAhead; ++s) load_w(s, s);
