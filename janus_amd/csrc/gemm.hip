@@ -388,19 +388,20 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
 #pragma unroll
       for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = p.route_w[id[rb]];
     }
+    // each row's slot offset, also before the first store (a divisor constant the compiler keeps in scratch would
+    // otherwise be reloaded, and waited for, between the stores)
+    long orow_off[kRowBlocks];
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb) {
+      const int tok = shared ? id[rb] : id[rb] / p.topk;
+      const int slot = shared ? p.topk : id[rb] - tok * p.topk;
+      orow_off[rb] = ((long)tok * p.nslots + slot) * N;
+    }
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
       const int m = rb * 16 + nl;
       if (rb >= nrb || m >= rows) continue;
-      int tok, slot;
-      if (shared) {
-        tok = id[rb];
-        slot = p.topk;
-      } else {
-        tok = id[rb] / p.topk;
-        slot = id[rb] - tok * p.topk;
-      }
-      float* orow = p.slots + ((long)tok * p.nslots + slot) * N + col0 + 4 * g;
+      float* orow = p.slots + orow_off[rb] + col0 + 4 * g;
       const float w = wt[rb];
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb)
