@@ -514,20 +514,25 @@ __global__ void __launch_bounds__(kSelThreads) router_select_kernel(
       for (int c = 0; c < kExactBatch; ++c) {
         pos[c] = 0;
         ids[c] = 0;
-        bnd[c] = 0.0;
         if (c < exact_batch(NHV) && f) {
           pos[c] = __builtin_ctzll(f);
           f &= f - 1;
           ids[c] = __builtin_amdgcn_readlane(ei, pos[c]);
-          bnd[c] = xnorm * p.wnorm[ids[c]] * (1.0 + 1e-6);
           n = c + 1;
         }
+      }
+      // the batch's norms and biases loaded together, outside the branches above (an unused entry reads expert 0)
+      float bb[kExactBatch];
+#pragma unroll
+      for (int c = 0; c < kExactBatch; ++c) {
+        bnd[c] = xnorm * p.wnorm[ids[c]] * (1.0 + 1e-6);
+        bb[c] = bias ? bias[ids[c]] : 0.f;
       }
       float l[kExactBatch];
       exact_logits<NHV>(xrow, H, w, ids, n, bnd, l);
 #pragma unroll
       for (int c = 0; c < kExactBatch; ++c)
-        if (c < n && lane == pos[c]) vi = bias ? l[c] + bias[ids[c]] : l[c];
+        if (c < n && lane == pos[c]) vi = bias ? l[c] + bb[c] : l[c];
     }
     r = lane_rank(vi, ei, nc);
     wave_sync();
