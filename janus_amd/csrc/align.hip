@@ -313,14 +313,21 @@ __global__ void __launch_bounds__(kRankThreads) align_rank_kernel(const IdxT* __
   const int base = blockIdx.x * kAlignChunk;
   if (base >= A) return;
   for (int e = tid; e < E; e += kRankThreads) cnt[e] = 0;
+  // the block's ids, loaded together before the passes below store ranks (an index past A re-reads the last id;
+  // dropped): a load after a possibly aliasing store, or under a branch, would cost a memory round trip each
+  constexpr int kPasses = kAlignChunk / kRankThreads;
+  long ids[kPasses];
+#pragma unroll
+  for (int r = 0; r < kPasses; ++r) {
+    const int a = base + r * kRankThreads + tid;
+    ids[r] = (long)idx[a < A ? a : A - 1];
+  }
   __syncthreads();
-  for (int round = 0; round < kAlignChunk / kRankThreads; ++round) {
+#pragma unroll
+  for (int round = 0; round < kPasses; ++round) {
     const int a = base + round * kRankThreads + tid;
-    int e = -1;
-    if (a < A) {
-      long v = (long)idx[a];
-      e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are dropped
-    }
+    const long v = ids[round];
+    const int e = (a < A && v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are dropped
     const Peers pr = wave_peers(e, nbits);
     const int rank_in_wave = pr.rank, n_peers = pr.count, leader = pr.leader;
     // Waves of this round take their turn in assignment order.
@@ -354,12 +361,23 @@ __global__ void __launch_bounds__(kScanThreads) align_scan_kernel(int* __restric
   __shared__ int cum[kMaxExperts];
   __shared__ int waves[16];
   const int tid = threadIdx.x;
+  // sixteen blocks' counts loaded together, then overwritten with the running offsets: a load written after a store
+  // into the same array waits for the loads before it, one memory round trip per block (a row past nb re-reads the
+  // last row, before any store of the batch; dropped)
+  constexpr int kBatch = 16;
   int c = 0;
   if (tid < E) {
-    for (int b = 0; b < nb; ++b) {
-      const int h = hist[(long)b * E + tid];
-      hist[(long)b * E + tid] = c;
-      c += h;
+    for (int b0 = 0; b0 < nb; b0 += kBatch) {
+      int h[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) h[u] = hist[(long)(b0 + u < nb ? b0 + u : nb - 1) * E + tid];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (b0 + u < nb) {
+          hist[(long)(b0 + u) * E + tid] = c;
+          c += h[u];
+        }
+      }
     }
     counts[tid] = c;
   }
