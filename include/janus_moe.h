@@ -4,7 +4,8 @@
  * Every entry point takes plain device pointers, sizes and a hipStream_t, launches its kernels on that stream
  * and returns at once: no allocation, no host synchronisation, no device-to-host read. Scratch memory comes from
  * the caller through `ws` / `ws_bytes` (ask the matching *_workspace_bytes function for the size). The calls are
- * re-entrant; the only process state is a thread-local error string. Return value 0 is success; any other value
+ * re-entrant; the process state is a thread-local error string and one status word per device that kernels set
+ * when something goes wrong on the device (janus_moe_device_status). Return value 0 is success; any other value
  * is an error code below, with a message in janus_moe_last_error().
  *
  * Tensor conventions (row-major, innermost dimension last, no padding):
@@ -55,6 +56,17 @@ JANUS_MOE_API int janus_moe_abi_version(void);
  * belong to the caller; at most 6. */
 JANUS_MOE_API int janus_moe_profile_events(void* const* events, int count);
 
+/* Sticky status of this library's kernels on the calling thread's current device. No counterpart in the reference,
+ * whose torch ops fail inside the call; these kernels run asynchronously and report here instead. Bits:
+ *   1  a down unit of the persistent experts launch gave up waiting for the h rows it reads (after
+ *      JANUS_MOE_SPIN_LIMIT polls of about 1 us, default 2^18, read at each launch; 0 gives up at once): the output
+ *      rows of that unit's tokens are NaN, never a silently wrong value;
+ *   2  an expert id outside [0, E) reached janus_moe_experts, janus_moe_experts_nvfp4 or janus_moe_align: that
+ *      assignment was dropped (it contributes nothing; the reference's index_add_ would have raised).
+ * Copies the word (every bit set on this device since it was last cleared) into out, device memory holding one
+ * int32, on the stream, then clears it when clear != 0. Read out after synchronising the stream. */
+JANUS_MOE_API int janus_moe_device_status(int32_t* out, int clear, janus_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------------------
  * Router.
  * janus_moe_router_prepare has no counterpart in the reference: it splits the fp32 router weight [E, H] once
@@ -96,7 +108,9 @@ JANUS_MOE_API int janus_moe_align(const int64_t* top_k_index, int S, int top_k, 
  *   out[s] = bf16( sum_j top_k_weights[s, j] * down_e( bf16(silu(gate_e(x[s])) * up_e(x[s])) ) ), e =
  *   top_k_index[s, j]; every dot product accumulates in fp32, the weighted sum over j is fp32 and rounded once.
  *   x [S, H] bf16, top_k_index [S, top_k] int64, top_k_weights [S, top_k] fp32, out [S, H] bf16.
- *   Requires H % 128 == 0 and I % 128 == 0. */
+ *   Requires H % 128 == 0 and I % 128 == 0, and below 4 GiB: S*H and (S*top_k + 15*E)*I bf16 values.
+ *   Ids must lie in [0, E): one outside is dropped (its term is left out of the sum) and reported as status bit 2
+ *   (janus_moe_device_status). */
 JANUS_MOE_API size_t janus_moe_experts_workspace_bytes(int S, int top_k, int E, int H, int I);
 JANUS_MOE_API int janus_moe_experts(const uint16_t* x, const int64_t* top_k_index, const float* top_k_weights,
                       const int32_t* gate_up_q, const uint16_t* gate_up_s, const int32_t* down_q,

@@ -19,10 +19,11 @@ AlignWorkspace carve_align(Carver& c, int A, int E);
 
 // sorted_ids [sorted_len] gets the permutation, the sentinel A everywhere else. Either expert_ids/total (reference tile
 // plan, `tiles` entries) or chunks/num_chunks (runs of at most chunk_rows rows of one expert) may be null. clear[0 ..
-// clear_n) is set to zero on the side (the counters of a later launch; null when clear_n == 0).
+// clear_n) is set to zero on the side (the counters of a later launch; null when clear_n == 0). Ids outside [0, E)
+// are dropped; status (null: no report) gets kStatusDroppedIds when one is.
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks, int* clear,
-                 int clear_n, hipStream_t stream);
+                 int clear_n, int* status, hipStream_t stream);
 
 }  // namespace janus

@@ -113,10 +113,17 @@ constexpr int kSmallWaves = kSmallBlock / kWave;
 constexpr int kSmallMaxA = kSmallBlock * 256;
 constexpr int kPlaceThreads = 1024;  // one thread per expert (E <= kMaxExperts)
 
+// An assignment whose expert id is outside [0, E) is dropped; with `status` non-null it also sets kStatusDroppedIds
+// there (the masked block routes padding tokens to id E on purpose and passes null).
+__device__ __forceinline__ void report_dropped(int* status, bool dropped) {
+  if (status && dropped) __hip_atomic_fetch_or(status, kStatusDroppedIds, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename IdxT>
 __global__ void __launch_bounds__(kSmallBlock) align_small_rank_kernel(const IdxT* __restrict__ idx, int A, int E,
                                                                        int nbits, int* __restrict__ hist,
-                                                                       int* __restrict__ local_rank) {
+                                                                       int* __restrict__ local_rank,
+                                                                       int* __restrict__ status) {
   __shared__ int wcnt[kSmallWaves][kMaxExperts];  // per-wave counts, then per-wave offsets within the block
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
   const int a = blockIdx.x * kSmallBlock + tid;
@@ -124,6 +131,7 @@ __global__ void __launch_bounds__(kSmallBlock) align_small_rank_kernel(const Idx
   if (a < A) {
     const long v = (long)idx[a];
     e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are dropped
+    report_dropped(status, e < 0);
   }
   const Peers pr = wave_peers(e, nbits);
   for (int i = tid; i < kSmallWaves * kMaxExperts; i += kSmallBlock) (&wcnt[0][0])[i] = 0;
@@ -223,7 +231,7 @@ template <typename IdxT, typename OutT>
 __global__ void __launch_bounds__(kPlaceThreads) align_one_kernel(
     const IdxT* __restrict__ idx, int A, int E, int nbits, int block, OutT* __restrict__ sorted_ids, int sorted_len,
     OutT* __restrict__ expert_ids, int tiles, OutT* __restrict__ total_out, int4* __restrict__ chunks,
-    int chunk_rows, int* __restrict__ num_chunks, int* __restrict__ clear, int clear_n) {
+    int chunk_rows, int* __restrict__ num_chunks, int* __restrict__ clear, int clear_n, int* __restrict__ status) {
   __shared__ int all_c[kMaxExperts], before_c[kMaxExperts];
   __shared__ int wcnt[kSmallWaves][kMaxExperts];  // per-wave counts of the block, then per-wave offsets
   __shared__ int cum[kMaxExperts];
@@ -242,6 +250,7 @@ __global__ void __launch_bounds__(kPlaceThreads) align_one_kernel(
   if (tid < kSmallBlock && a < A) {
     const long v = (long)idx[a];
     e = (v >= 0 && v < E) ? (int)v : -1;
+    report_dropped(status, e < 0);
   }
   __syncthreads();
   // every assignment, sixteen loads in flight per thread (one pass up to 16K assignments). The loads take no branch
@@ -304,7 +313,8 @@ __global__ void __launch_bounds__(kPlaceThreads) align_one_kernel(
 template <typename IdxT, typename OutT>
 __global__ void __launch_bounds__(kRankThreads) align_rank_kernel(const IdxT* __restrict__ idx, int A, int E, int nbits,
                                                                   int* __restrict__ hist, int* __restrict__ local_rank,
-                                                                  OutT* __restrict__ sorted_ids, int sorted_len) {
+                                                                  OutT* __restrict__ sorted_ids, int sorted_len,
+                                                                  int* __restrict__ status) {
   __shared__ int cnt[kMaxExperts];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
   // Side job, grid-stride: fill the output permutation with the sentinel.
@@ -328,6 +338,7 @@ __global__ void __launch_bounds__(kRankThreads) align_rank_kernel(const IdxT* __
     const int a = base + round * kRankThreads + tid;
     const long v = ids[round];
     const int e = (a < A && v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are dropped
+    report_dropped(status, a < A && e < 0);
     const Peers pr = wave_peers(e, nbits);
     const int rank_in_wave = pr.rank, n_peers = pr.count, leader = pr.leader;
     // Waves of this round take their turn in assignment order.
@@ -430,11 +441,11 @@ AlignWorkspace carve_align(Carver& c, int A, int E) {
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,
-                 int* clear, int clear_n, hipStream_t stream) {
+                 int* clear, int clear_n, int* status, hipStream_t stream) {
   if (A <= kOneMaxA) {
     hipLaunchKernelGGL((align_one_kernel<IdxT, OutT>), dim3(A > 0 ? ceil_div(A, kSmallBlock) : 1), dim3(kPlaceThreads),
                        0, stream, idx, A, E, expert_bits(E), block, sorted_ids, sorted_len, expert_ids, tiles, total,
-                       chunks, chunk_rows, num_chunks, clear, clear_n);
+                       chunks, chunk_rows, num_chunks, clear, clear_n, status);
     JANUS_LAUNCH_CHECK("align_one");
     return JANUS_MOE_OK;
   }
@@ -442,7 +453,7 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
     const int nb = ceil_div(A, kSmallBlock);
     if (nb > 0) {
       hipLaunchKernelGGL((align_small_rank_kernel<IdxT>), dim3(nb), dim3(kSmallBlock), 0, stream, idx, A, E,
-                         expert_bits(E), w.hist, w.local_rank);
+                         expert_bits(E), w.hist, w.local_rank, status);
       JANUS_LAUNCH_CHECK("align_small_rank");
     }
     hipLaunchKernelGGL((align_small_place_kernel<IdxT, OutT>), dim3(nb > 0 ? nb : 1), dim3(kPlaceThreads), 0, stream,
@@ -456,7 +467,7 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
   const int fill_blocks = ceil_div(sorted_len, kRankThreads * 8);
   if (fill_blocks > grid) grid = fill_blocks;
   hipLaunchKernelGGL((align_rank_kernel<IdxT, OutT>), dim3(grid), dim3(kRankThreads), 0, stream, idx, A, E,
-                     expert_bits(E), w.hist, w.local_rank, sorted_ids, sorted_len);
+                     expert_bits(E), w.hist, w.local_rank, sorted_ids, sorted_len, status);
   JANUS_LAUNCH_CHECK("align_rank");
   hipLaunchKernelGGL((align_scan_kernel<OutT>), dim3(1), dim3(kScanThreads), 0, stream, w.hist, nb, E, block, w.counts,
                      w.start, expert_ids, tiles, total, chunks, chunk_rows, num_chunks, clear, clear_n);
@@ -468,11 +479,11 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
 }
 
 template int launch_align<int64_t, int64_t>(const int64_t*, int, int, int, const AlignWorkspace&, int64_t*, int,
-                                            int64_t*, int, int64_t*, int4*, int, int*, int*, int, hipStream_t);
+                                            int64_t*, int, int64_t*, int4*, int, int*, int*, int, int*, hipStream_t);
 template int launch_align<int64_t, int>(const int64_t*, int, int, int, const AlignWorkspace&, int*, int, int*, int,
-                                        int*, int4*, int, int*, int*, int, hipStream_t);
+                                        int*, int4*, int, int*, int*, int, int*, hipStream_t);
 template int launch_align<int, int>(const int*, int, int, int, const AlignWorkspace&, int*, int, int*, int, int*,
-                                    int4*, int, int*, int*, int, hipStream_t);
+                                    int4*, int, int*, int*, int, int*, hipStream_t);
 
 }  // namespace janus
 
@@ -501,5 +512,6 @@ extern "C" int janus_moe_align(const int64_t* top_k_index, int S, int top_k, int
   AlignWorkspace w = carve_align(c, (int)A, E);
   const long tiles = (A + (long)E * (block - 1) + block - 1) / block;
   return launch_align<int64_t, int64_t>(top_k_index, (int)A, E, block, w, sorted_ids, (int)(tiles * block), expert_ids,
-                                        (int)tiles, total, nullptr, 0, nullptr, nullptr, 0, (hipStream_t)stream);
+                                        (int)tiles, total, nullptr, 0, nullptr, nullptr, 0, device_status_word(),
+                                        (hipStream_t)stream);
 }

@@ -7,6 +7,8 @@
 // workgroups exit), so a caller can capture the whole sequence in a HIP graph.
 #include <stdarg.h>
 
+#include <atomic>
+
 #include "align.h"
 #include "gemm.h"
 #include "norm.h"
@@ -33,6 +35,29 @@ void set_error(const char* fmt, ...) {
   vsnprintf(g_error, sizeof(g_error), fmt, ap);
   va_end(ap);
 }
+
+// One status word per device: every GPU the library runs on holds its own copy of this variable, at its own address.
+__device__ int g_status_word;
+
+int* device_status_word() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int*> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  int* p = cache[dev].load(std::memory_order_acquire);
+  if (!p) {
+    if (hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(g_status_word)) != hipSuccess) return nullptr;
+    cache[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+namespace {
+__global__ void read_status_kernel(int* __restrict__ status, int32_t* __restrict__ out, int clear) {
+  out[0] = *status;
+  if (clear) *status = 0;
+}
+}  // namespace
 
 namespace {
 
@@ -66,12 +91,19 @@ ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I,
   return w;
 }
 
-int check_expert_sizes(const char* who, int T, int H, int I, int E, int top_k) {
+int check_expert_sizes(const char* who, int T, int H, int I, int E, int top_k, int I_s = 0) {
   JANUS_REQUIRE(T >= 0 && H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0 && E > 0 && E <= kMaxExperts && top_k > 0 &&
                     top_k <= E && (long)T * top_k < (1l << 30),
                 JANUS_MOE_EINVAL,
                 "%s: unsupported sizes T=%d H=%d I=%d E=%d top_k=%d (need H %% 128 == 0, I %% 128 == 0, E <= %d, "
                 "top_k <= E)", who, T, H, I, E, top_k, kMaxExperts);
+  // The GEMMs address activation rows with 32-bit byte offsets from the buffer base: x rows (T x H bf16), the routed
+  // h rows (P = T*top_k + E*(kRowPad-1) padded rows x I) and the shared-expert h rows (T x I_s).
+  const long P = (long)T * top_k + (long)E * (kRowPad - 1);
+  JANUS_REQUIRE((long)T * H * 2 < (1l << 32) && P * I * 2 < (1l << 32) && (long)T * I_s * 2 < (1l << 32),
+                JANUS_MOE_EINVAL,
+                "%s: T=%d H=%d I=%d I_s=%d E=%d top_k=%d: an activation buffer (T*H, (T*top_k + 15*E)*I or T*I_s bf16 "
+                "values) reaches 4 GiB", who, T, H, I, I_s, E, top_k);
   return JANUS_MOE_OK;
 }
 
@@ -92,11 +124,15 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
                 const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
                 const ExpertsWorkspace& w, hipStream_t stream, int codec = 0, const float* gu_global = nullptr,
                 const float* dn_global = nullptr, const uint8_t* valid = nullptr,
-                const ServeEpilogue* serve = nullptr) {
+                const ServeEpilogue* serve = nullptr, const int64_t* check_ids = nullptr) {
   const int A = T * top_k;
+  int* status = device_status_word();
+  JANUS_REQUIRE(status, JANUS_MOE_ELAUNCH, "the device status word of this library could not be resolved");
   mark(1, stream);
+  // check_ids: the caller's own top-k ids (the experts entries). An id outside [0, E) is dropped by align, reported in
+  // the status word, and its slot skipped by the combine. The block path routes padding tokens to id E on purpose.
   int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
-                                   kChunkRows, w.num_chunks, w.sched, w.nsched, stream);
+                                   kChunkRows, w.num_chunks, w.sched, w.nsched, check_ids ? status : nullptr, stream);
   if (rc) return rc;
   const bool shared = I_s > 0;
   GemmParams p = {};
@@ -142,7 +178,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   d.route_w = route_w;
   d.gamma = gamma;
   mark(2, stream);
-  rc = launch_experts_fused(p, d, w.sched, stream);  // both GEMMs, one persistent launch
+  rc = launch_experts_fused(p, d, w.sched, status, stream);  // both GEMMs, one persistent launch
   if (rc == kNotFused) {
     rc = launch_gate_up(p, stream);
     if (rc) return rc;
@@ -157,7 +193,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
     rc = launch_combine_add_rmsnorm(w.slots, w.nslots, valid, serve->x_res, serve->norm_w, serve->eps, serve->valid,
                                     T, H, serve->n_out, stream);
   else
-    rc = launch_combine(w.slots, w.nslots, out, T, H, valid, stream);
+    rc = launch_combine(w.slots, w.nslots, out, T, H, valid, check_ids, top_k, E, stream);
   mark(5, stream);
   return rc;
 }
@@ -196,6 +232,15 @@ extern "C" int janus_moe_profile_events(void* const* events, int count) {
   return JANUS_MOE_OK;
 }
 
+extern "C" int janus_moe_device_status(int32_t* out, int clear, janus_stream_t stream) {
+  JANUS_REQUIRE(out, JANUS_MOE_EINVAL, "janus_moe_device_status: null pointer");
+  int* status = device_status_word();
+  JANUS_REQUIRE(status, JANUS_MOE_ELAUNCH, "janus_moe_device_status: the device status word could not be resolved");
+  hipLaunchKernelGGL(read_status_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, status, out, clear);
+  JANUS_LAUNCH_CHECK("janus_moe_device_status");
+  return JANUS_MOE_OK;
+}
+
 extern "C" size_t janus_moe_experts_workspace_bytes(int S, int top_k, int E, int H, int I) {
   if (S < 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
   Carver c(nullptr);
@@ -219,7 +264,8 @@ extern "C" int janus_moe_experts(const uint16_t* x, const int64_t* top_k_index, 
   ExpertsWorkspace w = carve_experts(c, S, top_k, E, H, I, 0);
   mark(0, (hipStream_t)stream);
   return run_experts<int64_t>(x, top_k_index, top_k_weights, gate_up_q, gate_up_s, down_q, down_s, nullptr, nullptr,
-                              nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w, (hipStream_t)stream);
+                              nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w, (hipStream_t)stream, 0, nullptr,
+                              nullptr, nullptr, nullptr, top_k_index);
 }
 
 extern "C" int janus_moe_experts_nvfp4(const uint16_t* x, const int64_t* top_k_index, const float* top_k_weights,
@@ -243,7 +289,8 @@ extern "C" int janus_moe_experts_nvfp4(const uint16_t* x, const int64_t* top_k_i
                               reinterpret_cast<const uint16_t*>(gate_up_scale),
                               reinterpret_cast<const int32_t*>(down), reinterpret_cast<const uint16_t*>(down_scale),
                               nullptr, nullptr, nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w,
-                              (hipStream_t)stream, /*codec=*/1, gate_up_global, down_global);
+                              (hipStream_t)stream, /*codec=*/1, gate_up_global, down_global, nullptr, nullptr,
+                              top_k_index);
 }
 
 extern "C" int janus_moe_dequant_nvfp4(const uint8_t* packed, const uint8_t* scale, const float* global, long rows,
@@ -275,7 +322,7 @@ int block_forward(const janus_moe_block_weights* wt, const uint16_t* x, const ui
                   const ServeEpilogue* serve) {
   JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward: null weights");
   const int H = wt->H, I = wt->I, E = wt->E, k = wt->top_k, I_s = wt->I_s;
-  int rc = check_expert_sizes("janus_moe_block_forward", T, H, I, E, k);
+  int rc = check_expert_sizes("janus_moe_block_forward", T, H, I, E, k, I_s > 0 ? I_s : 0);
   if (rc) return rc;
   rc = check_route_sizes(T, H, E, k);
   if (rc) return rc;

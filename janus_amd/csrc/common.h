@@ -39,6 +39,16 @@ void set_error(const char* fmt, ...);
     }                                                                                              \
   } while (0)
 
+// Sticky status bits the kernels set in the current device's status word (janus_moe_device_status reads and clears
+// it). The word is library state: a caller's workspace is fresh memory on every call and could not keep a bit until
+// it is read.
+constexpr int kStatusGaveUp = 1;      // a down unit of the persistent experts launch gave up waiting for its h rows;
+                                      // the output rows of its tokens are NaN
+constexpr int kStatusDroppedIds = 2;  // an expert id outside [0, E) reached janus_moe_experts(_nvfp4); it was skipped
+
+// The current device's status word (device memory), or null if the runtime cannot resolve it.
+int* device_status_word();
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -41,22 +41,23 @@ struct GemmParams {
   const float* gamma;         // down: shared-expert weight per token [T], null = 1
 };
 
-// Scheduler words of the persistent launch, zero before it (the align launch clears them): 8 ticket counters, an
-// error word, then one done counter per chunk.
+// Scheduler words of the persistent launch, zero before it (the align launch clears them): 8 ticket counters, 8 words
+// kept free, then one done counter per chunk.
 constexpr int kSchedWordsFixed = 16;
 __host__ __device__ inline int sched_words(int max_chunks, int n_shared_chunks) {
   return kSchedWordsFixed + max_chunks + n_shared_chunks;
 }
 constexpr int kNotFused = 1;  // launch_experts_fused: no persistent kernel for these sizes (or JANUS_MOE_SCHEDULE=split)
 
-// gate_up then down in one persistent launch (sched: sched_words() ints, zero); kNotFused when it does not apply.
-int launch_experts_fused(const GemmParams& gu, const GemmParams& dn, int* sched, hipStream_t stream);
+// gate_up then down in one persistent launch (sched: sched_words() ints, zero; status: the device status word, which
+// gets kStatusGaveUp if a wait gave up); kNotFused when it does not apply.
+int launch_experts_fused(const GemmParams& gu, const GemmParams& dn, int* sched, int* status, hipStream_t stream);
 int launch_gate_up(const GemmParams& p, hipStream_t stream);
 int launch_down(const GemmParams& p, hipStream_t stream);
 // out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32; 0 where valid[t] == 0 (valid null:
-// every token).
+// every token). ids (null: none) are the top-k ids [T, topk]: a slot j < topk whose id is outside [0, E) is skipped.
 int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, const uint8_t* valid,
-                   hipStream_t stream);
+                   const int64_t* ids, int topk, int E, hipStream_t stream);
 int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream);
 int launch_dequant_nvfp4(const uint8_t* q, const uint8_t* s, const float* gs, long rows, int K, uint16_t* out,
                          hipStream_t stream);

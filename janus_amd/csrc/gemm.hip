@@ -177,7 +177,7 @@ struct Codec<kNvfp4> {
 // nothing.
 template <int MODE, int NKB, int CODEC>
 __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams& p, int c, int slab,
-                                                                unsigned char* lds) {
+                                                                unsigned char* lds, bool poison = false) {
   using C = Codec<CODEC>;
   int tid = threadIdx.x;
   // the lane's index math is redone for every unit: kept from a caller's earlier iteration, it would hold registers
@@ -397,6 +397,10 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       const int slot = shared ? p.topk : id[rb] - tok * p.topk;
       orow_off[rb] = ((long)tok * p.nslots + slot) * N;
     }
+    if (poison) {  // this unit's h rows were not known to be complete: its rows become NaN instead of wrong values
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = __builtin_nanf("");
+    }
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
       const int m = rb * 16 + nl;
@@ -429,17 +433,18 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
 // the down units of early chunks fill the CUs that gate_up's last units leave idle.
 // A down unit waits until all gate_up units of its chunk have counted themselves done. It never waits for a unit
 // without a workgroup: each gate_up unit it depends on has a lower ticket of the same queue, so a running workgroup
-// took it, and gate_up units wait for nothing. The wait is bounded: past spin_limit polls it sets the error word and
-// goes on (the results are then wrong; the launch still ends).
+// took it, and gate_up units wait for nothing. The wait is bounded: after spin_limit polls (0: none) it gives up, sets
+// kStatusGaveUp in the device status word and writes NaN for its rows instead of a result computed on h rows that may
+// be incomplete; the launch still ends.
 constexpr int kSchedQueues = 8;   // ticket counters, one per XCD
-constexpr int kSchedError = 8;    // set when a wait gave up
 constexpr int kXccIdReg = 20 | (0 << 6) | ((16 - 1) << 11);  // s_getreg operand: HW_REG_XCC_ID, bits 0..15
 
 template <int NKB_GU, int NKB_DN, int CODEC>
 __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmParams gu, const GemmParams dn,
-                                                                  int* __restrict__ sched, int nq, int spin_limit) {
+                                                                  int* __restrict__ sched, int nq, int spin_limit,
+                                                                  int* __restrict__ status) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
-  __shared__ int ticket;
+  __shared__ int ticket, gave_up;
   // Every branch of this loop is uniform over a wave: wave 0 does the bookkeeping with all its lanes. A branch on the
   // thread id would give the loop a per-lane exit, and the compiler may then run the other lanes around the loop ahead
   // of lane 0, through barriers, on a stale ticket. The counters are bumped by buffer atomics that only lane 0 keeps
@@ -477,20 +482,23 @@ __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmPara
       const int u = t - ngu;
       const int c = __builtin_amdgcn_readfirstlane(q + nq * (u / dn.nslab));
       if (first_wave) {
+        int give_up = 0;
         for (int spins = 0;; ++spins) {
+          if (spins >= spin_limit) {
+            give_up = 1;
+            if (lane0) __hip_atomic_fetch_or(status, kStatusGaveUp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
           const int n = __builtin_amdgcn_readfirstlane(
               __hip_atomic_load(done + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
           if (n >= gu.nslab) break;
-          if (spins >= spin_limit) {
-            __hip_atomic_store(sched + kSchedError, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
           __builtin_amdgcn_s_sleep(2);
         }
         asm volatile("buffer_inv sc0" ::: "memory");  // this CU's L1 drops any stale copy of the chunk's h rows
+        gave_up = give_up;
       }
       __syncthreads();
-      gemm_unit<kDown, NKB_DN, CODEC>(dn, c, u % dn.nslab, lds);
+      gemm_unit<kDown, NKB_DN, CODEC>(dn, c, u % dn.nslab, lds, __builtin_amdgcn_readfirstlane(gave_up) != 0);
     }
     if (first_wave) ticket = __builtin_amdgcn_readfirstlane(next);
     __syncthreads();
@@ -500,8 +508,11 @@ __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmPara
 
 // out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order. The loads of up to 8 slots
 // are issued together before the additions. A padding token (valid[t] == 0) gets zeros and its slots are not read.
+// With ids (the caller's top-k ids [T, topk], int64), slot j < topk of token t counts only when its id is in [0, E):
+// the GEMMs never write the slot of a dropped assignment, so it is skipped (the load still issues, its value unused).
+template <bool kIds>
 __global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4,
-                               const uint8_t* __restrict__ valid) {
+                               const uint8_t* __restrict__ valid, const int64_t* __restrict__ ids, int topk, int E) {
   constexpr int kBatch = 8;
   const long n = (long)T * H4;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
@@ -510,8 +521,16 @@ __global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uin
       out[i] = make_uint2(0u, 0u);
       continue;
     }
+    uint32_t keep = ~0u;  // bit j: slot j counts
+    if (kIds) {
+      for (int j = 0; j < topk && j < 32; ++j) {
+        const int64_t e = ids[t * topk + j];
+        if (e < 0 || e >= E) keep &= ~(1u << j);
+      }
+    }
     const float4* src = slots + t * nslots * H4 + col;
     float4 s = src[0];
+    if (kIds && !(keep & 1u)) s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j0 = 1; j0 < nslots; j0 += kBatch) {
       f32x4 v[kBatch];
 #pragma unroll
@@ -520,7 +539,7 @@ __global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uin
           v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + (long)(j0 + j) * H4));
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        if (j0 + j < nslots) {
+        if (j0 + j < nslots && (!kIds || ((keep >> (j0 + j)) & 1u))) {
           s.x += v[j][0];
           s.y += v[j][1];
           s.z += v[j][2];
@@ -618,9 +637,11 @@ DeviceShape device_shape() {
 
 }  // namespace
 
-int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* sched, hipStream_t stream) {
+int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* sched, int* status,
+                         hipStream_t stream) {
   const char* env = getenv("JANUS_MOE_SCHEDULE");
   if (env && strcmp(env, "split") == 0) return kNotFused;
+  if (!status) return kNotFused;
   // a CU mask can leave an XCD without workgroups, and its queue would never drain
   if (getenv("HSA_CU_MASK") || getenv("ROC_GLOBAL_CU_MASK")) return kNotFused;
   GemmParams gu = gu_in, dn = dn_in;
@@ -633,13 +654,16 @@ int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* 
   dn.nslab = ceil_div(max(dn.N, dn.N_sh), slab_cols<kDown>());
   const int nkb_gu = gu.K / KS, nkb_dn = dn.K / KS;
   const dim3 g((unsigned)(2 * d.cus)), b(kThreads);
-  constexpr int kSpinLimit = 1 << 18;  // polls of about 1 us: a wait lasts at most one gate_up unit
+  // polls of about 1 us: a wait lasts at most one gate_up unit. JANUS_MOE_SPIN_LIMIT (a count, 0 = give up at once)
+  // lets a test force the give-up path from the host.
+  int spin_limit = 1 << 18;
+  if (const char* lim = getenv("JANUS_MOE_SPIN_LIMIT")) spin_limit = atoi(lim) < 0 ? 0 : atoi(lim);
   if (gu.codec == kInt4 && nkb_gu == 16 && nkb_dn == 4)
-    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kInt4>), g, b, 0, stream, gu, dn, sched, nq, kSpinLimit);
+    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kInt4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
   else if (gu.codec == kInt4 && nkb_gu == 4 && nkb_dn == 2)
-    hipLaunchKernelGGL((moe_experts_kernel<4, 2, kInt4>), g, b, 0, stream, gu, dn, sched, nq, kSpinLimit);
+    hipLaunchKernelGGL((moe_experts_kernel<4, 2, kInt4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
   else if (gu.codec == kNvfp4 && gu.gsc && dn.gsc && nkb_gu == 16 && nkb_dn == 4)
-    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kNvfp4>), g, b, 0, stream, gu, dn, sched, nq, kSpinLimit);
+    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kNvfp4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
   else
     return kNotFused;
   JANUS_LAUNCH_CHECK("w4a16 experts");
@@ -650,13 +674,21 @@ int launch_gate_up(const GemmParams& p, hipStream_t stream) { return launch_gemm
 int launch_down(const GemmParams& p, hipStream_t stream) { return launch_gemm<kDown>(p, stream); }
 
 int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, const uint8_t* valid,
-                   hipStream_t stream) {
+                   const int64_t* ids, int topk, int E, hipStream_t stream) {
   const long n4 = (long)T * (H / 4);
   if (n4 == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(!ids || (topk > 0 && topk <= 32), JANUS_MOE_EINVAL, "combine: top_k=%d with id checks (at most 32)",
+                topk);
   long blocks = (n4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, reinterpret_cast<const float4*>(slots),
-                     nslots, reinterpret_cast<uint2*>(out), T, H / 4, valid);
+  if (ids)
+    hipLaunchKernelGGL(combine_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(slots), nslots, reinterpret_cast<uint2*>(out), T, H / 4, valid,
+                       ids, topk, E);
+  else
+    hipLaunchKernelGGL(combine_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(slots), nslots, reinterpret_cast<uint2*>(out), T, H / 4, valid,
+                       nullptr, 0, 0);
   JANUS_LAUNCH_CHECK("combine");
   return JANUS_MOE_OK;
 }

@@ -52,6 +52,36 @@ def _workspace(nbytes: int, device: torch.device) -> Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
+# ---- device status ---------------------------------------------------------------------------------------------
+
+STATUS_GAVE_UP = 1       # a down unit of the experts launch gave up waiting for its h rows: its tokens' rows are NaN
+STATUS_DROPPED_IDS = 2   # an expert id outside [0, E) reached the experts or align op: the assignment was dropped
+_STATUS_TEXT = {STATUS_GAVE_UP: "a down unit of the experts launch gave up waiting for its h rows (its tokens' "
+                                "output rows are NaN)",
+                STATUS_DROPPED_IDS: "an expert id outside [0, num_experts) was dropped"}
+
+
+def device_status(device=None, clear: bool = True) -> Tensor:
+    """The device's sticky status word (janus_moe_device_status) as an int32 [1] tensor, copied on the current
+    stream (read it after a synchronisation) and cleared unless clear=False. Bits: STATUS_GAVE_UP, STATUS_DROPPED_IDS."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError("janus_moe device status lives on the GPU")
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().janus_moe_device_status(_ptr(out), int(bool(clear)), _stream(dev)), "janus_moe_device_status")
+    return out
+
+
+def check_device_status(device=None) -> None:
+    """Synchronises `device`, reads and clears its status word, and raises JanusMoeError naming every bit set since
+    the last read. The ops themselves never synchronise; a caller checks here at the point it chooses."""
+    word = int(device_status(device, clear=True).item())
+    if word:
+        bits = [text for bit, text in _STATUS_TEXT.items() if word & bit]
+        raise _lib.JanusMoeError(f"janus_moe device status {word:#x}: " + "; ".join(bits))
+
+
 # ---- router --------------------------------------------------------------------------------------------------
 
 @torch.library.custom_op("janus_moe::router_prepare", mutates_args=())

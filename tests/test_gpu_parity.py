@@ -99,12 +99,24 @@ def _route_case(cfg, gpu, seed=17, tokens=None):
     return idx.cpu().numpy(), w.cpu().numpy(), ridx, rw
 
 
-@pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf"])
+@pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf", "max"])
 def test_route_bit_exact(gpu, name):
+    """Every token of every config, T=16384 included: the selection and its slot order equal the oracle's rule."""
     cfg = synth.CONFIGS[name]
     idx, w, ridx, rw = _route_case(cfg, gpu)
     assert np.array_equal(idx, ridx), np.argwhere(idx != ridx)[:5]
     np.testing.assert_allclose(w, rw, rtol=1e-4, atol=1e-6)
+
+
+def test_route_then_align_at_the_largest_size(gpu):
+    """T=16384: the router's own selection fed to align (the three-launch schedule above 65,536 assignments) equals
+    the oracle's align of the oracle's selection, bit for bit."""
+    cfg = synth.CONFIGS["max"]
+    idx, _, ridx, _ = _route_case(cfg, gpu)
+    assert np.array_equal(idx, ridx)
+    got = align(torch.from_numpy(idx).to(gpu), cfg.E, 16)
+    for g, w, what in zip(got, O.align(ridx, cfg.E, 16), ("sorted_ids", "expert_ids", "total")):
+        assert np.array_equal(g.cpu().numpy(), w), what
 
 
 def test_route_ties_go_to_the_lower_expert(gpu):
@@ -190,8 +202,11 @@ def _block(cfg, gpu, seed=17):
     return L, blk
 
 
-@pytest.mark.parametrize("name,sample", [("tiny", None), ("short", None), ("headline", 48), ("zipf", 48), ("max", 32)])
+@pytest.mark.parametrize("name,sample", [("tiny", None), ("short", None), ("headline", 512), ("zipf", 512),
+                                         ("max", 512)])
 def test_block_matches_oracle(gpu, name, sample):
+    """The whole layer against the oracle: every token of the small configs, 512 tokens spread evenly over the large
+    ones (the oracle decodes every hit expert's weights for them; at these sizes that is nearly every expert)."""
     cfg = synth.CONFIGS[name]
     L, blk = _block(cfg, gpu)
     x = synth.activations(cfg)
@@ -292,7 +307,7 @@ def test_block_valid_mask_skips_padding_rows(gpu, name, rows):
             assert torch.equal(captured[mask], full[mask])
 
 
-@pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf"])
+@pytest.mark.parametrize("name", ["tiny", "short", "headline", "zipf", "max"])
 def test_persistent_schedule_equals_one_launch_per_gemm(gpu, name, monkeypatch):
     """Both GEMMs in one persistent launch (a ticket queue per XCD, down units waiting for their chunk's gate_up
     units) against one launch per GEMM: the same units in another order, so the same bits. The calls in a row reuse
@@ -352,6 +367,60 @@ def test_persistent_schedule_fused_moe_int4_and_nvfp4(gpu, S, monkeypatch):
                 out = call()
                 torch.cuda.synchronize()
                 assert torch.equal(out, split)
+
+
+def test_spin_limit_zero_gives_up_reports_and_poisons(gpu, monkeypatch):
+    """JANUS_MOE_SPIN_LIMIT=0 makes every down unit of the persistent launch give up before its first poll (the kernel
+    still ends normally): the device status reports it, every output row is NaN rather than a wrong number, and the
+    next call at the default limit is the normal result bit for bit with a clean status."""
+    cfg = synth.CONFIGS["short"]
+    _, blk = _block(cfg, gpu)
+    x = synth.activations(cfg).to(gpu)
+    with torch.no_grad():
+        good = blk(x).clone()
+        torch.cuda.synchronize()
+        ops.check_device_status(gpu)
+        monkeypatch.setenv("JANUS_MOE_SPIN_LIMIT", "0")
+        bad = blk(x)
+        torch.cuda.synchronize()
+        word = int(ops.device_status(gpu, clear=False).item())
+        assert word & ops.STATUS_GAVE_UP, word
+        assert torch.isnan(bad.float()).all()
+        with pytest.raises(ops._lib.JanusMoeError, match="gave up"):
+            ops.check_device_status(gpu)
+        assert int(ops.device_status(gpu).item()) == 0          # read and cleared above
+        monkeypatch.delenv("JANUS_MOE_SPIN_LIMIT")
+        again = blk(x)
+        torch.cuda.synchronize()
+        assert torch.equal(again, good)
+        ops.check_device_status(gpu)
+
+
+def test_fused_moe_drops_and_reports_out_of_range_ids(gpu):
+    """An id outside [0, E) in fused_moe's top_k_index: the assignment contributes nothing (the oracle with its weight
+    zeroed), the other rows are unaffected, and the device status reports the drop."""
+    S, E, H, I, k = 64, 16, 2048, 512, 8
+    cfg = synth.LayerConfig("case", T=S, H=H, E=E, k=k, I=I)
+    L = synth.layer(cfg, 11)
+    x = synth.activations(cfg, 11)
+    rng = np.random.default_rng(11)
+    idx = rng.integers(0, E, size=(S, k))
+    w = torch.softmax(torch.from_numpy(rng.standard_normal((S, k))), -1).float()
+    bad = idx.copy()
+    bad[5, 3], bad[17, 0], bad[40, 7] = E, -1, E + 100
+    torch.cuda.synchronize()
+    ops.device_status(gpu)                                       # start clean
+    out = fused_moe(x.to(gpu), torch.from_numpy(bad).to(gpu), w.to(gpu), L["gate_up_q"].to(gpu),
+                    L["gate_up_s"].to(gpu), None, L["down_q"].to(gpu), L["down_s"].to(gpu), None)
+    torch.cuda.synchronize()
+    assert int(ops.device_status(gpu).item()) & ops.STATUS_DROPPED_IDS
+    wz = w.numpy().copy()
+    for t, j in ((5, 3), (17, 0), (40, 7)):
+        wz[t, j] = 0.0
+    n = O.numpy_layer(L)
+    ref = O.bf16_round(O.expert_sum(bf16_np(x), idx, wz, n["gate_up_q"], n["gate_up_s"], n["down_q"], n["down_s"]))
+    assert_layer_close(bf16_np(out), ref, "dropped ids")
+    ops.check_device_status(gpu)
 
 
 def test_block_graph_captured_first_in_a_fresh_thread(gpu):

@@ -240,3 +240,18 @@ def test_cpu_baseline_port_matches_oracle():
     ref, _, _, _ = O.block_forward(O.numpy_layer(Lw), O.bf16_values(x), cfg.k)
     got = O.bf16_values(out)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
+
+
+def test_zipf_config_is_load_skewed():
+    """The Zipf(1.2) config's defining property: under the oracle's routing of its 4096 tokens the hottest expert
+    receives more than ten times the mean count (the mean is T * k / E = 128)."""
+    from janus_amd import synth
+    from oracle import oracle as O
+
+    cfg = synth.CONFIGS["zipf"]
+    L = synth.layer(cfg)
+    x = synth.activations(cfg)
+    idx, _, _ = O.route(O.bf16_values(x), L["router_w"].numpy(), cfg.k, L["router_bias"].numpy())
+    counts = np.bincount(idx.reshape(-1), minlength=cfg.E)
+    assert counts.sum() == cfg.T * cfg.k
+    assert counts.max() > 10 * counts.mean(), (counts.max(), counts.mean())
