@@ -180,6 +180,20 @@ JANUS_MOE_API int janus_moe_block_forward_masked(const janus_moe_block_weights* 
                                                  float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------
+ * janus_moe_block_forward_masked without a workspace argument. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Its scratch is a static device array of JANUS_MOE_NOALLOC_SCRATCH_BYTES per GPU (64 MiB, held until
+ * the process ends); a call whose janus_moe_block_workspace_bytes exceeds it returns JANUS_MOE_EWORKSPACE (at the
+ * 35B-A3B shape, H 2048, 256 experts top-8, I = I_s = 512, that is above about 700 tokens). Nothing is allocated.
+ * Every call on one GPU uses that GPU's array and leaves its contents behind (each call writes what it reads first),
+ * so calls that overlap in time on one GPU, from several streams or threads, race. Same outputs, bit for bit, as
+ * janus_moe_block_forward_masked. */
+#define JANUS_MOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+JANUS_MOE_API int janus_moe_block_forward_noalloc(const janus_moe_block_weights* w, const uint16_t* x,
+                                                  const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                                  float* topk_w, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
  * Replaces _add_norm (janus/hybrid.py:267-273, with _rmsnorm :250-254): x_out = residual + h in bf16 (torch's bf16 add:
  * the fp32 sum rounded once; h NULL = no add) and n_out = Qwen3_5RMSNorm(x_out) =
  * bf16(fp32(x) * rsqrt(mean(fp32(x)^2) + eps) * (1 + fp32(weight))), zeroed where valid[t] == 0 (valid NULL: no mask).

@@ -23,6 +23,7 @@ EXPORTS = (
     "janus_moe_add_rmsnorm", "janus_moe_block_forward_serve",
     "janus_moe_dequant", "janus_moe_profile_events",
     "janus_moe_experts_nvfp4", "janus_moe_dequant_nvfp4", "janus_moe_device_status",
+    "janus_moe_block_forward_noalloc",
 )
 
 _p, _i, _z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -61,6 +62,7 @@ _SIGNATURES = {
     "janus_moe_experts_nvfp4": (_i, [_p] * 9 + [_i] * 5 + [_p, _p, _z, _p]),
     "janus_moe_dequant_nvfp4": (_i, [_p, _p, _p, ctypes.c_long, _i, _p, _p]),
     "janus_moe_device_status": (_i, [_p, _i, _p]),
+    "janus_moe_block_forward_noalloc": (_i, [ctypes.POINTER(BlockWeights), _p, _p, _i, _p, _p, _p, _p]),
 }
 
 _handle = None

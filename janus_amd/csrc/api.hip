@@ -357,6 +357,40 @@ extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt,
   return block_forward(wt, x, valid, T, out, topk_idx, topk_w, ws, ws_bytes, (hipStream_t)stream, nullptr);
 }
 
+namespace {
+// The scratch of janus_moe_block_forward_noalloc: a file-scope device array, one copy per GPU the library runs on,
+// held until the process ends. In host code `scratch` names a host-side stand-in, not device memory: the device
+// address comes from hipGetSymbolAddress, once per device with that device current, and only that address is used.
+__device__ __align__(256) unsigned char scratch[JANUS_MOE_NOALLOC_SCRATCH_BYTES];
+
+void* scratch_address() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = cache[dev].load(std::memory_order_acquire);
+  if (!p) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    cache[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+}  // namespace
+
+extern "C" int janus_moe_block_forward_noalloc(const janus_moe_block_weights* wt, const uint16_t* x,
+                                               const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                               float* topk_w, janus_stream_t stream) {
+  JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward_noalloc: null weights");
+  const size_t need = janus_moe_block_workspace_bytes(T, wt->H, wt->I, wt->E, wt->top_k, wt->I_s);
+  JANUS_REQUIRE(need <= JANUS_MOE_NOALLOC_SCRATCH_BYTES, JANUS_MOE_EWORKSPACE,
+                "janus_moe_block_forward_noalloc: T=%d needs %zu bytes of scratch; the static array holds %zu (use "
+                "janus_moe_block_forward_masked with a workspace)", T, need, (size_t)JANUS_MOE_NOALLOC_SCRATCH_BYTES);
+  void* ws = scratch_address();
+  JANUS_REQUIRE(ws, JANUS_MOE_ELAUNCH, "janus_moe_block_forward_noalloc: hipGetSymbolAddress of the scratch failed");
+  return block_forward(wt, x, valid, T, out, topk_idx, topk_w, ws, JANUS_MOE_NOALLOC_SCRATCH_BYTES,
+                       (hipStream_t)stream, nullptr);
+}
+
 extern "C" int janus_moe_block_forward_serve(const janus_moe_block_weights* wt, const uint16_t* x,
                                              const uint16_t* h_attn, const uint16_t* post_norm_w, float post_eps,
                                              const uint16_t* next_norm_w, float next_eps, const uint8_t* valid,
