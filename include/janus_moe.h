@@ -108,7 +108,7 @@ JANUS_MOE_API int janus_moe_align(const int64_t* top_k_index, int S, int top_k, 
  *   out[s] = bf16( sum_j top_k_weights[s, j] * down_e( bf16(silu(gate_e(x[s])) * up_e(x[s])) ) ), e =
  *   top_k_index[s, j]; every dot product accumulates in fp32, the weighted sum over j is fp32 and rounded once.
  *   x [S, H] bf16, top_k_index [S, top_k] int64, top_k_weights [S, top_k] fp32, out [S, H] bf16.
- *   Requires H % 128 == 0 and I % 128 == 0, and below 4 GiB: S*H and (S*top_k + 15*E)*I bf16 values.
+ *   Requires H % 128 == 0 and I % 128 == 0, and below 2 GiB: S*H and (S*top_k + 15*E)*I bf16 values.
  *   Ids must lie in [0, E): one outside is dropped (its term is left out of the sum) and reported as status bit 2
  *   (janus_moe_device_status). */
 JANUS_MOE_API size_t janus_moe_experts_workspace_bytes(int S, int top_k, int E, int H, int I);

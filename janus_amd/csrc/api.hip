@@ -100,10 +100,10 @@ int check_expert_sizes(const char* who, int T, int H, int I, int E, int top_k, i
   // The GEMMs address activation rows with 32-bit byte offsets from the buffer base: x rows (T x H bf16), the routed
   // h rows (P = T*top_k + E*(kRowPad-1) padded rows x I) and the shared-expert h rows (T x I_s).
   const long P = (long)T * top_k + (long)E * (kRowPad - 1);
-  JANUS_REQUIRE((long)T * H * 2 < (1l << 32) && P * I * 2 < (1l << 32) && (long)T * I_s * 2 < (1l << 32),
+  JANUS_REQUIRE((long)T * H * 2 < (1l << 31) && P * I * 2 < (1l << 31) && (long)T * I_s * 2 < (1l << 31),
                 JANUS_MOE_EINVAL,
                 "%s: T=%d H=%d I=%d I_s=%d E=%d top_k=%d: an activation buffer (T*H, (T*top_k + 15*E)*I or T*I_s bf16 "
-                "values) reaches 4 GiB", who, T, H, I, I_s, E, top_k);
+                "values) reaches 2 GiB", who, T, H, I, I_s, E, top_k);
   return JANUS_MOE_OK;
 }
 
@@ -147,6 +147,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.n_shared_chunks = shared ? ceil_div(T, kChunkRows) : 0;
   // gate_up
   p.a = x;
+  p.a_bytes = (uint32_t)((size_t)T * H * 2);
   p.q = guq;
   p.s = gus;
   p.gsc = gu_global;
@@ -163,6 +164,8 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   GemmParams d = p;
   d.a = w.h;
   d.a_sh = w.h_sh;
+  d.a_bytes = (uint32_t)((size_t)w.P * I * 2);
+  d.a_sh_bytes = (uint32_t)((size_t)T * I_s * 2);
   d.q = dq;
   d.s = ds;
   d.gsc = dn_global;

@@ -17,6 +17,7 @@ constexpr int kRowPad = 16;                   // every expert's rows start at a 
 struct GemmParams {
   const uint16_t* a;          // gate_up: x [T, K]; down: h of the routed rows [P, K]
   const uint16_t* a_sh;       // down: h of the shared expert [T, K_sh]
+  uint32_t a_bytes, a_sh_bytes;  // sizes of a and a_sh (below 2 GiB): loads past them read zeros
   const int* sorted_ids;      // assignment id at each permuted position (< A on real rows)
   int topk, A, T;
   int codec;                  // 0: int4 group-128 (q words, s bf16 [E, N, K/128]); 1: NVFP4 (q bytes, s e4m3

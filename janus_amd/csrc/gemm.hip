@@ -27,7 +27,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kColBlocks = 4;
 constexpr int KS = 128;                                      // k per pipeline stage: one scale group
-constexpr int kStages = 2;                                   // weight ring depth: loads run one stage ahead
+constexpr int kStages = 3;                                   // activation and weight rings: loads run two stages ahead
 constexpr int kRowBytes = KS * 2;                            // one activation row of a stage (bf16)
 constexpr int kSlotBytes = kChunkRows * kRowBytes;           // one LDS activation buffer
 
@@ -50,34 +50,42 @@ __device__ __forceinline__ void static_for(F&& f) {
 // included): LDS writes are completed first, and the asm keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// The k pipeline. Activations: global -> registers (one stage ahead) -> LDS double buffer, written once the stage
-// before has been consumed. Weight words and scales: a kStages-slot register ring, loads kStages - 1 stages ahead. Every load is an
-// ordinary compiler-tracked load; with NKB fixed the loop is unrolled, so the compiler's waits are exact counts.
-//   load_a(kb) / store_a(buf)          stage kb's activation rows into registers / registers into LDS buffer buf
-//   load_b(slot, kb)                   stage kb's weight words and scales into ring slot `slot`
-//   compute(slot, buf)                 MFMAs of the stage held in ring slot `slot` and LDS buffer buf
-template <int NKB, typename LoadA, typename StoreA, typename LoadB, typename Compute>
-__device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool active, LoadA&& load_a,
-                                                                   StoreA&& store_a, LoadB&& load_b,
+#define JANUS_LDS __attribute__((address_space(3)))
+
+// The k pipeline over nkb stages of KS k. Activations go from global memory straight into LDS (buffer loads that write
+// LDS, no register staging) and weight words and scales into registers; both are rings of kStages slots, slot = stage
+// mod kStages, and each stage's loads are issued kStages - 1 stages ahead, activations first. The compiler does not
+// order a buffer-to-LDS load before later LDS reads, so the pipeline does: before the barrier that opens stage kb,
+// every wave consumes stage kb's weight registers in an empty asm, for which the compiler waits with an exact count
+// (every global load here is one it tracks). A wave's loads complete in issue order, so its stage-kb activation loads,
+// issued before those weights, have landed too; the barrier then publishes the whole tile. The same barrier tells
+// every wave that all reads of the stage before are done, so its slot can be refilled right after it.
+//   issue_a(slot, kb) / issue_b(slot, kb)   stage kb's activation tile into LDS slot / weights into register slot
+//   wait_b(slot, kb)                        the empty asm on stage kb's weight registers (ring slot `slot`)
+//   compute(slot, kb)                       MFMAs of stage kb, held in slot `slot`
+template <int NKB, typename IssueA, typename IssueB, typename WaitB, typename Compute>
+__device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool active, IssueA&& issue_a,
+                                                                   IssueB&& issue_b, WaitB&& wait_b,
                                                                    Compute&& compute) {
+  constexpr int ahead = kStages - 1;
   auto step = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    constexpr int ahead = kStages - 1;  // weight loads run this many stages ahead
-    if (kb + ahead < nkb) load_b(Slot<(slot + ahead) % kStages>{}, kb + ahead);
-    if (active) compute(slot_c, kb & 1);
-    if (kb + 1 < nkb) {
-      store_a((kb + 1) & 1);
-      if (kb + 2 < nkb) load_a(kb + 2);
-    }
+    wait_b(slot_c, kb);
     lds_barrier();
+    if (kb + ahead < nkb) {
+      issue_a(Slot<(slot + ahead) % kStages>{}, kb + ahead);
+      asm volatile("" ::: "memory");  // the compiler may not hoist the weight loads above the activation loads
+      issue_b(Slot<(slot + ahead) % kStages>{}, kb + ahead);
+    }
+    if (active) compute(slot_c, kb);
   };
-  load_a(0);
-  static_for<kStages - 1>([&](auto s_c) __attribute__((always_inline)) {
-    if (decltype(s_c)::value < nkb) load_b(s_c, decltype(s_c)::value);
+  static_for<ahead>([&](auto s_c) __attribute__((always_inline)) {
+    if (decltype(s_c)::value < nkb) {
+      issue_a(s_c, decltype(s_c)::value);
+      asm volatile("" ::: "memory");
+      issue_b(s_c, decltype(s_c)::value);
+    }
   });
-  store_a(0);
-  if (nkb > 1) load_a(1);
-  lds_barrier();
   if constexpr (NKB > 0) {
     static_for<NKB>([&](auto kb_c) __attribute__((always_inline)) {
       step(Slot<decltype(kb_c)::value % kStages>{}, decltype(kb_c)::value);
@@ -217,36 +225,45 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   const bool active = col0 < out_cols;
   const int nrb = (rows + 15) / 16;
 
-  // ---- activation rows this lane stages: pass r covers rows 16r..16r+15, this wave rows 16r + 4w + (lane >> 4), 16
-  // lanes per row each taking one 16-byte chunk (chunk lane & 15) ----
-  // 32-bit byte offsets from wave-uniform bases (SGPR base + VGPR offset addressing) keep the pointer state small.
+  // ---- activation rows this lane loads: load r covers rows 16r..16r+15, this wave's instruction rows 16r + 4w ..
+  // 16r + 4w + 3 (64 lanes x 16 bytes = 4 rows of a stage, written to LDS in lane order). Lane l writes LDS chunk
+  // position l & 15 of row 16r + 4w + (l >> 4); position q of row m holds global chunk q ^ (m & 15), so the 16 lanes of
+  // a fragment read (one chunk, 16 rows) hit 16 different bank groups. The load of a row past the chunk gets an offset
+  // beyond the buffer, which the hardware answers with zeros. Byte offsets are 32-bit (the host bounds the buffers
+  // below 2 GiB). A routed gate_up unit's rows are tokens looked up through sorted_ids, all six lookups issued before
+  // the first is used (a load selected against another value under a branch would be waited for at once).
   const unsigned char* abase;
-  if (MODE == kGateUp)
+  uint32_t abytes;
+  if (MODE == kGateUp) {
     abase = reinterpret_cast<const unsigned char*>(p.a);
-  else
+    abytes = p.a_bytes;
+  } else {
     abase = reinterpret_cast<const unsigned char*>(shared ? p.a_sh : p.a);
-  // Padding rows re-read row 0: finite values, results discarded. A routed gate_up unit's rows are tokens looked up
-  // through sorted_ids, all six lookups issued before the first is used (the branch on `shared` stays outside the
-  // loops: a load selected against another value under it would be waited for at once).
+    abytes = shared ? p.a_sh_bytes : p.a_bytes;
+  }
+  const __amdgpu_buffer_rsrc_t arsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(abase), (short)0, (int)abytes, 0x00020000);
+  constexpr uint32_t kOutside = 0x80000000u;  // past every activation buffer
+  const int lrow = 4 * wave + (lane >> 4);    // this lane's row within a load's 16 (row & 15 of every row it loads)
+  const uint32_t achunk = (uint32_t)(((lane & 15) ^ lrow) * 16);
   uint32_t aoff[kRowBlocks];
   if (MODE == kGateUp && !shared) {
     int id[kRowBlocks];
 #pragma unroll
     for (int r = 0; r < kRowBlocks; ++r) {
-      const int row = 16 * r + 4 * wave + (lane >> 4);
+      const int row = 16 * r + lrow;
       id[r] = p.sorted_ids[pos0 + (row < rows ? row : 0)];
     }
 #pragma unroll
     for (int r = 0; r < kRowBlocks; ++r)
-      aoff[r] = (uint32_t)(id[r] / p.topk) * (uint32_t)(K * 2) + (lane & 15) * 16;
+      aoff[r] = (16 * r + lrow < rows) ? (uint32_t)(id[r] / p.topk) * (uint32_t)(K * 2) + achunk : kOutside;
   } else {
 #pragma unroll
     for (int r = 0; r < kRowBlocks; ++r) {
-      const int row = 16 * r + 4 * wave + (lane >> 4);
-      aoff[r] = (uint32_t)(pos0 + (row < rows ? row : 0)) * (uint32_t)(K * 2) + (lane & 15) * 16;
+      const int row = 16 * r + lrow;
+      aoff[r] = row < rows ? (uint32_t)(pos0 + row) * (uint32_t)(K * 2) + achunk : kOutside;
     }
   }
-  const int arow0 = 4 * wave + (lane >> 4);  // this lane's row in pass 0
 
   // ---- weight rows of this lane, one per column block (an idle wave reads row 0 and discards it) ----
   const unsigned char* wbase = reinterpret_cast<const unsigned char*>(wq);
@@ -275,34 +292,57 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   const int nkb = NKB > 0 ? NKB : K / KS;
   u32x4 bw[kStages][kColBlocks];
   uint32_t sc[kStages][kColBlocks];
+  // int4 scales with the k loop unrolled: one 8-byte load per column block brings the bf16 scales of four stages (the
+  // row's groups 4m .. 4m + 3 are adjacent), issued with the weights of stage 4m; two batches are live at a time
+  constexpr bool kBatchScales = CODEC == kInt4 && NKB >= 4 && NKB % 4 == 0;
+  u32x2 scb[2][kColBlocks];
 
-  u32x4 areg[kRowBlocks];  // native vectors: an array of HIP's uint4 struct is not promoted to registers
-  auto load_a = [&](int kb) __attribute__((always_inline)) {
+  // the LDS destination is wave-uniform (it goes to M0) and the stage's k offset rides in the SGPR offset
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  auto issue_a = [&](auto slot_c, int kb) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    unsigned char* dst = lds + slot * kSlotBytes + (4 * uwave) * kRowBytes;
 #pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r) areg[r] = *reinterpret_cast<const u32x4*>(abase + aoff[r] + kb * (KS * 2));
-  };
-  auto store_a = [&](int buf) __attribute__((always_inline)) {
-    unsigned char* dst = lds + buf * kSlotBytes;
-#pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r) {
-      const int row = 16 * r + arow0;
-      *reinterpret_cast<u32x4*>(dst + row * kRowBytes + (((lane & 15) ^ (row & 15)) * 16)) = areg[r];
-    }
+    for (int r = 0; r < kRowBlocks; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (JANUS_LDS void*)(dst + 16 * r * kRowBytes), 16, aoff[r],
+                                               kb * (KS * 2), 0, 0);
   };
   auto load_b = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
       bw[slot][cb] = *reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2));
-      sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
+      if constexpr (kBatchScales) {
+        if (kb % 4 == 0) scb[(kb / 4) & 1][cb] = *reinterpret_cast<const u32x2*>(sbase + soff[cb] + kb * 2);
+      } else {
+        sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
+      }
     }
   };
-  auto compute = [&](auto slot_c, int buf) __attribute__((always_inline)) {
+  // stage kb's scale bits of column block cb (the batched form keeps the bf16 bits in either half of a word)
+  auto stage_scale = [&](auto slot_c, int kb, int cb) __attribute__((always_inline)) -> uint32_t {
     constexpr int slot = decltype(slot_c)::value;
-    const unsigned char* base = lds + buf * kSlotBytes;
+    if constexpr (kBatchScales) {
+      const u32x2 v = scb[(kb / 4) & 1][cb];
+      const uint32_t word = (kb & 2) ? v[1] : v[0];
+      return (kb & 1) ? word >> 16 : word & 0xFFFFu;
+    } else {
+      return sc[slot][cb];
+    }
+  };
+  auto wait_b = [&](auto slot_c, int kb) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const u32x4 w0 = bw[slot][0], w1 = bw[slot][1], w2 = bw[slot][2], w3 = bw[slot][3];
+    const uint32_t s0 = stage_scale(slot_c, kb, 0), s1 = stage_scale(slot_c, kb, 1), s2 = stage_scale(slot_c, kb, 2),
+                   s3 = stage_scale(slot_c, kb, 3);
+    asm volatile("" ::"v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(s0), "v"(s1), "v"(s2), "v"(s3));
+  };
+  auto compute = [&](auto slot_c, int kb) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    const unsigned char* base = lds + slot * kSlotBytes;
     typename C::State scl[kColBlocks];
 #pragma unroll
-    for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = C::make(sc[slot][cb], gq[cb]);
+    for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = C::make(stage_scale(slot_c, kb, cb), gq[cb]);
 #pragma unroll
     for (int t = 0; t < KS / 32; ++t) {
       // every row block's fragment is read before the decode, which covers the LDS latency (rows past the chunk hold
@@ -331,7 +371,8 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       }
     }
   };
-  run_pipeline<NKB>(nkb, active, load_a, store_a, load_b, compute);
+  static_assert(kColBlocks == 4, "wait_b lists every column block");
+  run_pipeline<NKB>(nkb, active, issue_a, load_b, wait_b, compute);
   if (!active) return;
 
   // ---- epilogue: lane holds rows 16 rb + nl, columns 16 cb + 4 g + i ----
@@ -419,7 +460,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
 // c mod 8, so they share its L2.
 template <int MODE, int NKB, int CODEC>
 __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * kSlotBytes];
   const int xcd = blockIdx.x & 7, within = blockIdx.x >> 3;
   const int c = (within / p.nslab) * 8 + xcd;
   if (c >= p.n_shared_chunks + p.max_chunks) return;
@@ -443,7 +484,7 @@ template <int NKB_GU, int NKB_DN, int CODEC>
 __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmParams gu, const GemmParams dn,
                                                                   int* __restrict__ sched, int nq, int spin_limit,
                                                                   int* __restrict__ status) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kSlotBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * kSlotBytes];
   __shared__ int ticket, gave_up;
   // Every branch of this loop is uniform over a wave: wave 0 does the bookkeeping with all its lanes. A branch on the
   // thread id would give the loop a per-lane exit, and the compiler may then run the other lanes around the loop ahead
