@@ -88,4 +88,11 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+#define JANUS_LDS __attribute__((address_space(3)))
+
+// Barrier without the memory fence __syncthreads() adds (which would wait for every outstanding load, prefetches
+// included): LDS reads and writes are completed first, and the asm keeps the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace janus

@@ -46,12 +46,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(std::make_integer_sequence<int, N>{}, static_cast<F&&>(f));
 }
 
-// Barrier without the memory fence __syncthreads() adds (which would wait for every outstanding load, prefetches
-// included): LDS writes are completed first, and the asm keeps the compiler from moving memory accesses across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-#define JANUS_LDS __attribute__((address_space(3)))
-
 // The k pipeline over nkb stages of KS k. Activations go from global memory straight into LDS (buffer loads that write
 // LDS, no register staging) and weight words and scales into registers; both are rings of kStages slots, slot = stage
 // mod kStages, and each stage's loads are issued kStages - 1 stages ahead, activations first. The compiler does not

@@ -6,7 +6,8 @@
 namespace janus {
 
 struct RouteWorkspace {
-  float* partial;  // [ceil(H/512), T, ceil(E/64)*64] approximate-logit partial sums
+  float* partial;  // [k ranges, T, padded E] approximate-logit partial sums
+  float2* xstat;   // [k ranges, T] (||x||^2, x . w_shared_gate) partial sums
 };
 
 size_t router_prep_bytes(int E, int H);
