@@ -173,13 +173,25 @@ struct Codec<kNvfp4> {
 // weight registers are exact (a runtime loop makes it wait for every outstanding load); 0 = runtime K.
 //
 // One work unit: chunk c (c < n_shared_chunks: shared-expert tokens c * kChunkRows.., else routed chunk
-// c - n_shared_chunks) times column slab `slab`. lds: the workgroup's LDS double buffer of activation tiles,
-// [buffer][row][16-byte chunk] with chunk position = chunk ^ (row & 15): the 16 lanes of a fragment read (same chunk, 16
-// rows) hit 16 different bank groups. Uniform over the workgroup; a unit past the chunk list or the columns does
-// nothing.
+// c - n_shared_chunks) times column slab `slab`. lds: the workgroup's ring of activation tiles, one array per slot
+// (separate arrays let the compiler see that a load into one slot does not write the slot being read, so its wait for
+// the loads into LDS before a read covers only that slot's), each [row][16-byte chunk] with chunk position =
+// chunk ^ (row & 15): the 16 lanes of a fragment read (same chunk, 16 rows) hit 16 different bank groups. Uniform over
+// the workgroup; a unit past the chunk list or the columns does nothing.
+// The activation ring: kStages separate LDS arrays (see gemm_unit).
+struct LdsRing {
+  unsigned char* s0;
+  unsigned char* s1;
+  unsigned char* s2;
+  template <typename S>
+  __device__ __forceinline__ unsigned char* slot(S) const {
+    return S::value == 0 ? s0 : S::value == 1 ? s1 : s2;
+  }
+};
+
 template <int MODE, int NKB, int CODEC>
 __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams& p, int c, int slab,
-                                                                unsigned char* lds, bool poison = false) {
+                                                                LdsRing lds, bool poison = false) {
   using C = Codec<CODEC>;
   int tid = threadIdx.x;
   // the lane's index math is redone for every unit: kept from a caller's earlier iteration, it would hold registers
@@ -295,7 +307,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
   auto issue_a = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    unsigned char* dst = lds + slot * kSlotBytes + (4 * uwave) * kRowBytes;
+    unsigned char* dst = lds.slot(slot_c) + (4 * uwave) * kRowBytes;
 #pragma unroll
     for (int r = 0; r < kRowBlocks; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (JANUS_LDS void*)(dst + 16 * r * kRowBytes), 16, aoff[r],
@@ -333,7 +345,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   };
   auto compute = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
-    const unsigned char* base = lds + slot * kSlotBytes;
+    const unsigned char* base = lds.slot(slot_c);
     typename C::State scl[kColBlocks];
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) scl[cb] = C::make(stage_scale(slot_c, kb, cb), gq[cb]);
@@ -454,11 +466,12 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
 // c mod 8, so they share its L2.
 template <int MODE, int NKB, int CODEC>
 __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * kSlotBytes];
+  static_assert(kStages == 3, "one array per ring slot");
+  __shared__ __attribute__((aligned(16))) unsigned char lds0[kSlotBytes], lds1[kSlotBytes], lds2[kSlotBytes];
   const int xcd = blockIdx.x & 7, within = blockIdx.x >> 3;
   const int c = (within / p.nslab) * 8 + xcd;
   if (c >= p.n_shared_chunks + p.max_chunks) return;
-  gemm_unit<MODE, NKB, CODEC>(p, c, within % p.nslab, lds);
+  gemm_unit<MODE, NKB, CODEC>(p, c, within % p.nslab, LdsRing{lds0, lds1, lds2});
 }
 
 // Both GEMMs in one persistent launch of two workgroups per CU. The work units sit in one queue per XCD: queue q holds
@@ -478,7 +491,9 @@ template <int NKB_GU, int NKB_DN, int CODEC>
 __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmParams gu, const GemmParams dn,
                                                                   int* __restrict__ sched, int nq, int spin_limit,
                                                                   int* __restrict__ status) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * kSlotBytes];
+  static_assert(kStages == 3, "one array per ring slot");
+  __shared__ __attribute__((aligned(16))) unsigned char lds0[kSlotBytes], lds1[kSlotBytes], lds2[kSlotBytes];
+  const LdsRing lds{lds0, lds1, lds2};
   __shared__ int ticket, gave_up;
   // Every branch of this loop is uniform over a wave: wave 0 does the bookkeeping with all its lanes. A branch on the
   // thread id would give the loop a per-lane exit, and the compiler may then run the other lanes around the loop ahead
