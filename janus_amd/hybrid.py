@@ -12,7 +12,10 @@ CPU tensor raises, as the reference's Triton kernel would: nothing falls back si
 """
 from __future__ import annotations
 
+import json
 import os
+import re
+from pathlib import Path
 
 import torch
 import torch.nn.functional as F
@@ -246,39 +249,41 @@ class _PackedExperts(nn.Module):
         return out.view(S, k, -1).float().sum(1).to(hidden_states.dtype)
 
     def _bmm(self, hidden_states, top_k_index, top_k_weights, gate_up, down):
-        """Every expert's tokens padded to the busiest expert's count, one bmm per projection, scatter-add
-        (janus/hybrid.py:574-598)."""
-        S, k = top_k_index.shape
-        flat = top_k_index.reshape(-1)
-        order = torch.argsort(flat, stable=True)
-        counts = torch.bincount(flat, minlength=self.num_experts)
-        starts = counts.cumsum(0) - counts
-        width = int(counts.max()) if counts.numel() else 0
-        slot = torch.arange(S * k, device=order.device) - starts[flat[order]]
-        index = torch.full((self.num_experts, width), S, dtype=torch.long, device=order.device)
-        index[flat[order], slot] = order // k
-        x = torch.cat([hidden_states, hidden_states.new_zeros(1, hidden_states.shape[1])])[index]
-        h = self._apply_gate(torch.bmm(x, gate_up.transpose(1, 2).to(x.dtype).contiguous()))
-        y = torch.bmm(h, down.transpose(1, 2).to(x.dtype).contiguous())
-        valid = index.reshape(-1) < S
-        weight = torch.zeros(self.num_experts * width, dtype=hidden_states.dtype, device=order.device)
-        weight[flat[order] * width + slot] = top_k_weights.reshape(-1)[order].to(hidden_states.dtype)
-        out = torch.zeros_like(hidden_states)
-        out.index_add_(0, index.reshape(-1)[valid], (y.reshape(-1, y.shape[-1]) * weight[:, None])[valid])
-        return out
+        """The reference's CPU path (janus/hybrid.py:574-598), same result: every expert gets a tile of `capacity`
+        rows (the busiest expert's assignment count) holding its tokens in assignment order, zeros below; each
+        projection is one batched GEMM over the tiles; every assignment's output row, times its routing weight, is
+        added into its token's row."""
+        n_assign, n_exp = top_k_index.numel(), self.num_experts
+        expert = top_k_index.reshape(-1)
+        token = torch.arange(n_assign, device=expert.device) // top_k_index.shape[1]
+        # an assignment's row in its expert's tile: how many earlier assignments went to the same expert
+        seen = F.one_hot(expert, n_exp).cumsum(0)
+        row = seen.gather(1, expert[:, None]).squeeze(1) - 1
+        capacity = int(seen[-1].max()) if n_assign else 0
+        tiles = hidden_states.new_zeros(n_exp, capacity, hidden_states.shape[1])
+        tiles[expert, row] = hidden_states[token]
+        inner = self._apply_gate(torch.bmm(tiles, gate_up.transpose(1, 2).to(tiles.dtype).contiguous()))
+        result = torch.bmm(inner, down.transpose(1, 2).to(tiles.dtype).contiguous())
+        scaled = result[expert, row] * top_k_weights.reshape(-1, 1).to(result.dtype)
+        return torch.zeros_like(hidden_states).index_add_(0, token, scaled.to(hidden_states.dtype))
 
     def _eager(self, hidden_states, top_k_index, top_k_weights, gate_up, down):
-        """Per hit expert: gather its tokens, the two GEMMs, scatter-add (janus/hybrid.py:600-618)."""
+        """The reference's per-expert loop (janus/hybrid.py:600-618), same result: the assignments ordered by expert
+        once (token order within an expert), then expert by expert in id order its two linears on its tokens' rows,
+        and the rows, times their routing weights, added into their tokens' rows."""
+        n_exp, k = self.num_experts, top_k_index.shape[1]
+        by_expert = torch.argsort(top_k_index.reshape(-1), stable=True)
+        ends = torch.bincount(top_k_index.reshape(-1), minlength=n_exp).cumsum(0).tolist()
+        token, weight = by_expert // k, top_k_weights.reshape(-1)[by_expert]
         out = torch.zeros_like(hidden_states)
-        hits = torch.bincount(top_k_index.flatten(), minlength=self.num_experts).tolist()
-        for e, count in enumerate(hits):
-            if count == 0:
-                continue
-            token, slot = torch.where(top_k_index == e)
-            x = hidden_states[token]
-            h = self._apply_gate(F.linear(x, gate_up[e].to(x.dtype)))
-            y = F.linear(h, down[e].to(x.dtype))
-            out.index_add_(0, token, (y * top_k_weights[token, slot, None]).to(out.dtype))
+        begin = 0
+        for e, end in enumerate(ends):
+            if end > begin:
+                rows = token[begin:end]
+                inner = self._apply_gate(F.linear(hidden_states[rows], gate_up[e].to(hidden_states.dtype)))
+                result = F.linear(inner, down[e].to(hidden_states.dtype))
+                out.index_add_(0, rows, (result * weight[begin:end, None]).to(out.dtype))
+            begin = end
         return out
 
 
@@ -339,94 +344,91 @@ class NVFP4Experts(_PackedExperts):
 MODEL_PREFIX = "model.language_model."
 
 
-def load_nvfp4(lm, snapshot, dtype=torch.bfloat16):
-    """Fill a meta-device Qwen3_5MoeTextModel `lm` from a ModelOpt NVFP4 checkpoint directory, as
-    janus/hybrid.py:641-701 does. The checkpoint keeps each expert's `gate_proj`/`up_proj`/`down_proj` as NVFP4
-    (`weight` uint8 pairs, `weight_scale` e4m3 per 16, `weight_scale_2` one fp32), the shared expert's linears likewise,
-    the attention and linear-attention projections as fp8 e4m3 with one fp32 `weight_scale`, and everything else in
-    bf16.
-      - every layer's experts become `NVFP4Experts` with stacks allocated before `to_empty` (so no bf16 stack ever
-        exists) and filled per expert: gate rows 0..I-1, up rows I..2I-1, each projection's `weight_scale_2` spread over
-        its rows (the shape table of janus/hybrid.py:658-660);
-      - NVFP4 linears become `NVFP4Linear`, packed as stored; fp8 projections are dequantised once to `dtype`;
-      - `input_scale` (activation calibration) is not used, and keys outside `model.language_model.` (vision tower,
-        MTP head, lm_head) are skipped.
-    Shards are read on the CPU. Raises ValueError when a model parameter, or a piece of an expert stack, is left
-    unfilled."""
-    import json
-    from pathlib import Path
+_EXPERT_PROJS = ("gate_proj", "up_proj", "down_proj")
+_NVFP4_FIELDS = ("weight", "weight_scale", "weight_scale_2")
+_EXPERT_PIECE = re.compile(r"layers\.(\d+)\.mlp\.experts\.(\d+)\.(gate_proj|up_proj|down_proj)")
 
+
+def _expert_piece(stack: NVFP4Experts, e: int, proj: str, field: str, t: torch.Tensor, inter: int) -> None:
+    """Copy one checkpoint tensor of expert e into its stack: gate_proj to gate_up rows [0, I), up_proj to [I, 2I),
+    down_proj to down; the fp32 `weight_scale_2` spread over the rows it scales."""
+    target = {"weight": ("gate_up", "down"), "weight_scale": ("gate_up_scale", "down_scale"),
+              "weight_scale_2": ("gate_up_global", "down_global")}[field][proj == "down_proj"]
+    buf = getattr(stack, target)[e]
+    if proj != "down_proj":
+        buf = buf[:inter] if proj == "gate_proj" else buf[inter:]
+    buf.copy_(t.reshape(()).expand(buf.shape) if field == "weight_scale_2" else t)
+
+
+def load_nvfp4(lm, snapshot, dtype=torch.bfloat16):
+    """Fill a meta-device Qwen3_5MoeTextModel `lm` from a ModelOpt NVFP4 checkpoint directory (the reference's
+    janus/hybrid.py:641-701). The checkpoint keeps each expert's `gate_proj`/`up_proj`/`down_proj` as NVFP4 (`weight`
+    uint8 pairs, `weight_scale` e4m3 per 16, `weight_scale_2` one fp32), the shared expert's linears likewise, the
+    attention and linear-attention projections as fp8 e4m3 with one fp32 `weight_scale`, and everything else in bf16.
+      - every layer's experts become `NVFP4Experts`, allocated before `to_empty` (no bf16 stack ever exists) and
+        filled one checkpoint tensor at a time (gate rows 0..I-1, up rows I..2I-1, `weight_scale_2` over its rows);
+      - NVFP4 linears become `NVFP4Linear`, packed as stored; fp8 projections are dequantised once to `dtype`;
+      - `input_scale` (activation calibration) is not used; keys outside `model.language_model.` (vision tower, MTP
+        head, lm_head) are skipped.
+    Shards are read on the CPU. Raises ValueError naming the tensors the model needs and the shards lack (a model
+    parameter, a piece of an expert stack, or part of a quantised linear)."""
     from safetensors import safe_open
 
     snapshot = Path(snapshot)
-    weight_map = json.loads((snapshot / "model.safetensors.index.json").read_text())["weight_map"]
+    shard_of = json.loads((snapshot / "model.safetensors.index.json").read_text())["weight_map"]
     cfg = lm.config
-    E, I, H = cfg.num_experts, cfg.moe_intermediate_size, cfg.hidden_size
+    n_exp, inter, hid = cfg.num_experts, cfg.moe_intermediate_size, cfg.hidden_size
+    e4m3 = torch.float8_e4m3fn
+    stacks = []
     for layer in lm.layers:
-        act = layer.mlp.experts.act_fn
-        e4m3 = torch.float8_e4m3fn
-        layer.mlp.experts = NVFP4Experts(
-            torch.empty(E, 2 * I, H // 2, dtype=torch.uint8), torch.empty(E, 2 * I, H // FP4_BLOCK, dtype=e4m3),
-            torch.empty(E, 2 * I, 1), torch.empty(E, H, I // 2, dtype=torch.uint8),
-            torch.empty(E, H, I // FP4_BLOCK, dtype=e4m3), torch.empty(E, H, 1), act)
+        stacks.append(NVFP4Experts(
+            torch.empty(n_exp, 2 * inter, hid // 2, dtype=torch.uint8),
+            torch.empty(n_exp, 2 * inter, hid // FP4_BLOCK, dtype=e4m3), torch.empty(n_exp, 2 * inter, 1),
+            torch.empty(n_exp, hid, inter // 2, dtype=torch.uint8), torch.empty(n_exp, hid, inter // FP4_BLOCK, dtype=e4m3),
+            torch.empty(n_exp, hid, 1), layer.mlp.experts.act_fn))
+        layer.mlp.experts = stacks[-1]
     lm.to_empty(device="cpu")
     lm.rotary_emb = type(lm.rotary_emb)(config=cfg)  # its inv_freq buffers are not persistent: to_empty left them empty
-    modules = dict(lm.named_modules())
+    module_at = dict(lm.named_modules())
 
-    shards: dict[str, list[str]] = {}
-    for key, shard in weight_map.items():
-        if key.startswith(MODEL_PREFIX):
-            shards.setdefault(shard, []).append(key[len(MODEL_PREFIX):])
-    filled, expert_pieces, quantised = set(), set(), {}
-    stack_of = {"weight": ("gate_up", "down"), "weight_scale": ("gate_up_scale", "down_scale"),
-                "weight_scale_2": ("gate_up_global", "down_global")}
-    for shard in sorted(shards):
+    # every tensor the model needs, crossed off as it arrives
+    needed = {name for name, _ in lm.named_parameters()}
+    needed.update(f"layers.{li}.mlp.experts.{e}.{proj}.{field}" for li in range(len(stacks)) for e in range(n_exp)
+                  for proj in _EXPERT_PROJS for field in _NVFP4_FIELDS)
+    held: dict[str, dict[str, torch.Tensor]] = {}  # quantised linears: their parts, until every part has arrived
+    per_shard: dict[str, list[str]] = {}
+    for key, shard in shard_of.items():
+        if key.startswith(MODEL_PREFIX) and not key.endswith(".input_scale"):
+            per_shard.setdefault(shard, []).append(key[len(MODEL_PREFIX):])
+    for shard, names in sorted(per_shard.items()):
         with safe_open(str(snapshot / shard), "pt", device="cpu") as f:
-            for name in sorted(shards[shard]):
-                module, _, leaf = name.rpartition(".")
-                if leaf == "input_scale":
-                    continue
+            for name in sorted(names):
                 t = f.get_tensor(MODEL_PREFIX + name)
-                if ".mlp.experts." in module:
-                    owner, _, rest = module.rpartition(".experts.")
-                    index, proj = rest.split(".")
-                    experts = modules[owner + ".experts"]
-                    gu_name, dn_name = stack_of[leaf]
-                    if proj == "down_proj":
-                        dst = getattr(experts, dn_name)[int(index)]
-                    else:
-                        rows = slice(0, I) if proj == "gate_proj" else slice(I, 2 * I)
-                        dst = getattr(experts, gu_name)[int(index), rows]
-                    dst.copy_(t.reshape(()).expand(dst.shape) if leaf == "weight_scale_2" else t)
-                    expert_pieces.add((owner, int(index), proj, leaf))
-                elif leaf in ("weight_scale", "weight_scale_2") or t.dtype in (torch.uint8, torch.float8_e4m3fn):
-                    quantised.setdefault(module, {})[leaf] = t
+                path, _, field = name.rpartition(".")
+                piece = _EXPERT_PIECE.fullmatch(path)
+                if piece:
+                    _expert_piece(stacks[int(piece[1])], int(piece[2]), piece[3], field, t, inter)
+                    needed.discard(name)
+                elif field.startswith("weight_scale") or t.dtype in (torch.uint8, e4m3):
+                    held.setdefault(path, {})[field] = t
                 else:
-                    getattr(modules[module], leaf).data = t.to(dtype)
-                    filled.add(name)
-    incomplete = []
-    for module, parts in quantised.items():
-        owner, _, leaf = module.rpartition(".")
-        nvfp4 = "weight_scale_2" in parts or ("weight" in parts and parts["weight"].dtype == torch.uint8)
-        need = ("weight", "weight_scale", "weight_scale_2") if nvfp4 else ("weight", "weight_scale")
-        if any(n not in parts for n in need):
-            incomplete += [f"{module}.{n}" for n in need if n not in parts]
-            continue
-        if parts["weight"].dtype == torch.uint8:  # NVFP4: kept packed, the nn.Linear replaced
-            setattr(modules[owner], leaf, NVFP4Linear(parts["weight"], parts["weight_scale"], parts["weight_scale_2"]))
-        else:  # fp8 with one fp32 scale: dequantised once
-            modules[module].weight.data = (parts["weight"].float() * parts["weight_scale"].float()).to(dtype)
-            filled.add(module + ".weight")
-
-    missing = incomplete + [n for n, _ in lm.named_parameters() if n not in filled]
-    pieces = [(p, leaf) for p in ("gate_proj", "up_proj", "down_proj") for leaf in ("weight", "weight_scale",
-                                                                                   "weight_scale_2")]
-    for i in range(len(lm.layers)):
-        owner = f"layers.{i}.mlp"
-        missing += [f"{owner}.experts.{e}.{p}.{leaf}" for e in range(E) for p, leaf in pieces
-                    if (owner, e, p, leaf) not in expert_pieces]
-    if missing:
-        raise ValueError(f"{snapshot}: {len(missing)} model tensors not in the shards, e.g. {missing[:5]}")
+                    getattr(module_at[path], field).data = t.to(dtype)
+                    needed.discard(name)
+    for path, parts in held.items():
+        packed = parts.get("weight") is not None and parts["weight"].dtype == torch.uint8
+        fields = _NVFP4_FIELDS if packed or "weight_scale_2" in parts else _NVFP4_FIELDS[:2]
+        if not all(field in parts for field in fields):
+            continue  # the linear's weight stays in `needed`, and the error below names it
+        parent, _, attr = path.rpartition(".")
+        if packed:
+            setattr(module_at[parent], attr, NVFP4Linear(parts["weight"], parts["weight_scale"], parts["weight_scale_2"]))
+        else:
+            module_at[path].weight.data = (parts["weight"].float() * parts["weight_scale"].float()).to(dtype)
+        needed.discard(path + ".weight")
+    if needed:
+        missing = sorted(needed)
+        raise ValueError(f"load_nvfp4: {len(missing)} tensors the model needs are not in {snapshot}: "
+                         f"{', '.join(missing[:5])}{' ...' if len(missing) > 5 else ''}")
     return lm
 
 
