@@ -61,15 +61,33 @@ def layer_work(cfg, idx: np.ndarray) -> dict:
     return dict(n_hit=n_hit, flops=flops, bytes=layer_bytes, ex_bytes=ex_bytes, ex_flops=ex_flops)
 
 
-def cpu_baseline(layer, x, k, budget_s: float = 30.0) -> dict:
-    from oracle import cpu_bmm
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else what platform reports."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def rel_l2(a, b) -> float:
+    a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def cpu_baseline(layer, x, k, gpu_out: torch.Tensor, budget_s: float = 30.0, n_check: int = 16) -> dict:
+    """The reference's CPU algorithm timed on the host cores, and checked in the same run: its output on the first
+    n_check tokens against the oracle's, and on every token against the HIP path's output."""
+    from oracle import cpu_bmm, oracle
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     lay = {n: (None if t is None else t.cpu()) for n, t in layer.items()}
     xc = x.cpu()
     t0 = time.perf_counter()
-    cpu_bmm.layer_forward(lay, xc, k)          # warm-up
+    out = cpu_bmm.layer_forward(lay, xc, k)    # warm-up, and the output checked below
     first = time.perf_counter() - t0
     calls = max(1, min(3, int(budget_s / max(first, 1e-3)) - 1))
     times = []
@@ -78,9 +96,13 @@ def cpu_baseline(layer, x, k, budget_s: float = 30.0) -> dict:
         cpu_bmm.layer_forward(lay, xc, k)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
-    return {"value": x.shape[0] / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+    tokens = np.arange(min(n_check, x.shape[0]))
+    want = oracle.block_forward(oracle.numpy_layer(lay), oracle.bf16_values(xc), k, tokens=tokens)[0]
+    check = {"tokens_vs_oracle": int(tokens.size), "rel_l2_vs_oracle": rel_l2(out[tokens].float().numpy(), want),
+             "rel_l2_vs_hip": rel_l2(out.float().numpy(), gpu_out.float().cpu().numpy())}
+    return {"value": x.shape[0] / t, "unit": "tokens/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
             "sample": f"full layer at T={x.shape[0]}: median of {calls} calls after 1 warm-up "
-                      f"({t:.2f} s per call, torch CPU, {platform.processor() or platform.machine()})"}
+                      f"({t:.2f} s per call, torch CPU on {cores} threads)", "check": check}
 
 
 def make_layer(name: str, dev: torch.device):
@@ -197,28 +219,55 @@ def _pmc_child(args) -> int:
     return 0
 
 
-def _counter_per_dispatch(db: Path, counter: str, kernel_substr: str) -> float:
-    """Mean over dispatches of `counter` (summed over its hardware instances) for kernels whose name matches the regular
-    expression kernel_substr."""
+def _counters_per_dispatch(db: Path, counters: list[str], kernel_substr: str) -> dict:
+    """Per counter: (mean over dispatches of the value summed over its hardware instances, instances per dispatch),
+    for kernels whose name matches the regular expression kernel_substr."""
     con = sqlite3.connect(db)
-    per = {}
+    per = {c: {} for c in counters}
+    inst = {c: {} for c in counters}
     for name, disp, cn, v in con.execute("select name, dispatch_id, counter_name, counter_value from pmc_events"):
-        if cn == counter and re.search(kernel_substr, name.replace(" ", "")):
-            per[disp] = per.get(disp, 0.0) + v
-    if not per:
-        raise RuntimeError(f"no {counter} samples for {kernel_substr} in {db}")
-    return float(np.mean(list(per.values())))
+        if cn in per and re.search(kernel_substr, name.replace(" ", "")):
+            per[cn][disp] = per[cn].get(disp, 0.0) + v
+            inst[cn][disp] = inst[cn].get(disp, 0) + 1
+    out = {}
+    for c in counters:
+        if not per[c]:
+            raise RuntimeError(f"no {c} samples for {kernel_substr} in {db}")
+        out[c] = (float(np.mean(list(per[c].values()))), int(max(inst[c].values())))
+    return out
 
 
-def _profile(counter: str, child_args: list[str], kernel_substr: str, timeout: int = 150) -> float:
+def _profile_counters(counters: list[str], child_args: list[str], kernel_substr: str, timeout: int = 150) -> dict:
     with tempfile.TemporaryDirectory() as tmp:
-        cmd = ["rocprofv3", "--pmc", counter, "-d", tmp, "-o", "run", "--", sys.executable, str(HERE / "bench.py"),
+        cmd = ["rocprofv3", "--pmc", *counters, "-d", tmp, "-o", "run", "--", sys.executable, str(HERE / "bench.py"),
                "--pmc-child", *child_args]
         subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=timeout, check=True)
         dbs = sorted(Path(tmp).rglob("*results.db"))
         if not dbs:
             raise RuntimeError("rocprofv3 wrote no results database")
-        return _counter_per_dispatch(dbs[0], counter, kernel_substr)
+        return _counters_per_dispatch(dbs[0], counters, kernel_substr)
+
+
+def _profile(counter: str, child_args: list[str], kernel_substr: str, timeout: int = 150) -> float:
+    return _profile_counters([counter], child_args, kernel_substr, timeout)[counter][0]
+
+
+BUSY_COUNTERS = ["SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU", "SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY",
+                 "GRBM_GUI_ACTIVE"]
+
+
+def pmc_busy(config: str, simds: int) -> dict:
+    """Issue counters of the experts launch, one rocprofv3 pass: MFMA pipe busy as a fraction of every SIMD's cycles
+    over the dispatch (SQ_VALU_MFMA_BUSY_CYCLES sums the busy cycles of all SIMDs; GRBM_GUI_ACTIVE counts the
+    dispatch's cycles once per instance), MFMA and VALU instructions (per wave64 instruction) and the share of wave
+    cycles spent waiting for an instruction's operands or a barrier."""
+    c = _profile_counters(BUSY_COUNTERS, ["--config", config], EXPERTS_KERNEL)
+    cycles = c["GRBM_GUI_ACTIVE"][0] / c["GRBM_GUI_ACTIVE"][1]
+    return {"mfma_insts": c["SQ_INSTS_MFMA"][0], "valu_insts": c["SQ_INSTS_VALU"][0], "cycles": cycles,
+            "mfma_busy_frac": c["SQ_VALU_MFMA_BUSY_CYCLES"][0] / (simds * cycles),
+            "wave_wait_frac": c["SQ_WAIT_INST_ANY"][0] / max(c["SQ_WAVE_CYCLES"][0], 1.0),
+            "command": f"rocprofv3 --pmc {' '.join(BUSY_COUNTERS)} -d <dir> -o run -- python3 bench.py --pmc-child "
+                       f"--config {config}"}
 
 
 def pmc_traffic(config: str) -> dict:
@@ -262,7 +311,11 @@ def main() -> int:
         blk(x)                                  # router prep, first launch
         _, _, idx = blk.gate(x)
     torch.cuda.synchronize()
-    work = layer_work(cfg, idx.cpu().numpy())
+    idx_np = idx.cpu().numpy()
+    work = layer_work(cfg, idx_np)
+    rows = np.bincount(idx_np.reshape(-1), minlength=cfg.E)
+    routing = {"experts_hit": int(np.count_nonzero(rows)), "max_rows": int(rows.max()),
+               "mean_rows": float(rows.mean()), "max_over_mean": float(rows.max() / rows.mean())}
     L = _lib.lib()
 
     def step():
@@ -336,9 +389,16 @@ def main() -> int:
                             f"write {t['write_bytes']:.4g} B per launch")
         except Exception as exc:  # no profiler on this machine: the entry stays null, with the reason
             traffic_note = f"unavailable: {type(exc).__name__}: {exc}"[:300]
+    busy = None
+    if not split and not args.no_pmc:
+        try:
+            busy = pmc_busy(args.config, 4 * torch.cuda.get_device_properties(dev).multi_processor_count)
+        except Exception as exc:
+            busy = f"unavailable: {type(exc).__name__}: {exc}"[:300]
     kernel = "w4a16_gemm_kernel<gate_up> + <down> (split)" if split else "moe_experts_kernel (gate_up + down)"
     roof.update({"traffic": traffic, "kernel": kernel, "algorithmic_bytes": work["ex_bytes"],
-                 "algorithmic_flops": work["ex_flops"], "avg_us": stage_us["experts"], "traffic_source": traffic_note})
+                 "algorithmic_flops": work["ex_flops"], "avg_us": stage_us["experts"], "traffic_source": traffic_note,
+                 "issue_counters": busy})
 
     result = {
         "metric": METRIC, "value": cfg.T / t_step, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -353,11 +413,12 @@ def main() -> int:
                            "bound": "hbm" if work["bytes"] / HBM_PEAK >= work["flops"] / MFMA_BF16_PEAK else "mfma",
                            "flops": work["flops"], "bytes": work["bytes"], "n_hit": work["n_hit"]},
         "stages_us": stage_us,
+        "routing": routing,
         "graph_tokens_per_s": cfg.T / graph_s, "graph_ms_per_step": graph_s * 1e3,
     }
     result["variants_us"] = variant_timings(cfg, x, blk, dev)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(layer, x, cfg.k)
+        result["cpu_baseline"] = cpu_baseline(layer, x, cfg.k, step())
     print(json.dumps(result))
     return 0
 

@@ -106,6 +106,9 @@ def test_route_bit_exact(gpu, name):
     idx, w, ridx, rw = _route_case(cfg, gpu)
     assert np.array_equal(idx, ridx), np.argwhere(idx != ridx)[:5]
     np.testing.assert_allclose(w, rw, rtol=1e-4, atol=1e-6)
+    if name == "zipf":  # the workload's defining skew: its hottest expert takes over 10x the mean load
+        rows = np.bincount(idx.reshape(-1), minlength=cfg.E)
+        assert rows.max() > 10 * rows.mean(), (rows.max(), rows.mean())
 
 
 def test_route_then_align_at_the_largest_size(gpu):
