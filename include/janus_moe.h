@@ -106,7 +106,9 @@ JANUS_MOE_API int janus_moe_align(const int64_t* top_k_index, int S, int top_k, 
  * Replaces fused_moe(x, top_k_index, top_k_weights, gate_up, ..., down, ...) (janus/moe_w4a16.py:122-140) and
  * NVFP4Experts.forward (janus/hybrid.py:551-572) for the int4 group-128 codec:
  *   out[s] = bf16( sum_j top_k_weights[s, j] * down_e( bf16(silu(gate_e(x[s])) * up_e(x[s])) ) ), e =
- *   top_k_index[s, j]; every dot product accumulates in fp32, the weighted sum over j is fp32 and rounded once.
+ *   top_k_index[s, j]; every dot product accumulates in fp32; each weighted term is held as int16 codes with one
+ *   fp32 scale per 64 columns (error at most 2^-16 of the block's largest |term|), and the sum over j is fp32,
+ *   rounded once.
  *   x [S, H] bf16, top_k_index [S, top_k] int64, top_k_weights [S, top_k] fp32, out [S, H] bf16.
  *   Requires H % 128 == 0 and I % 128 == 0, and below 2 GiB: S*H and (S*top_k + 15*E)*I bf16 values.
  *   Ids must lie in [0, E): one outside is dropped (its term is left out of the sum) and reported as status bit 2
@@ -146,7 +148,7 @@ JANUS_MOE_API int janus_moe_dequant(const int32_t* q, const uint16_t* s, long ro
 /* ------------------------------------------------------------------------------------------------------------
  * Replaces Qwen3_5MoeSparseMoeBlock.forward (transformers models/qwen3_5_moe/modeling_qwen3_5_moe.py:787-798)
  * with int4 expert and shared-expert weights: router, routed experts, shared expert scaled by
- * sigmoid(x . shared_gate), all summed in fp32 and rounded to bf16 once. */
+ * sigmoid(x . shared_gate), all summed in fp32 and rounded to bf16 once (each term held as in janus_moe_experts). */
 typedef struct janus_moe_block_weights {
   int H, I, E, top_k;             /* hidden, routed intermediate, experts, experts per token */
   int I_s;                        /* shared-expert intermediate; 0 = no shared expert */
@@ -184,7 +186,7 @@ JANUS_MOE_API int janus_moe_block_forward_masked(const janus_moe_block_weights* 
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Its scratch is a static device array of JANUS_MOE_NOALLOC_SCRATCH_BYTES per GPU (64 MiB, held until
  * the process ends); a call whose janus_moe_block_workspace_bytes exceeds it returns JANUS_MOE_EWORKSPACE (at the
- * 35B-A3B shape, H 2048, 256 experts top-8, I = I_s = 512, that is above about 700 tokens). Nothing is allocated.
+ * 35B-A3B shape, H 2048, 256 experts top-8, I = I_s = 512, that is above 1,134 tokens). Nothing is allocated.
  * Every call on one GPU uses that GPU's array and leaves its contents behind (each call writes what it reads first),
  * so calls that overlap in time on one GPU, from several streams or threads, race. Same outputs, bit for bit, as
  * janus_moe_block_forward_masked. */

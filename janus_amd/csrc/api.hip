@@ -68,7 +68,8 @@ struct ExpertsWorkspace {
   int* num_chunks;  // [1]
   uint16_t* h;      // [P, I]
   uint16_t* h_sh;   // [T, I_s]
-  float* slots;     // [T, nslots, H] weighted expert outputs
+  int16_t* slots;    // [T, nslots, H] weighted expert outputs: int16 codes (slot format of gemm.h)
+  float* slot_scale;  // [T, nslots, H / kSlotBlock] their block scales
   int* sched;       // [nsched] counters of the persistent GEMM launch, cleared by align
   int P, C, nslots, nsched;
 };
@@ -87,7 +88,8 @@ ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I,
   w.h = c.take<uint16_t>((size_t)w.P * I);
   w.h_sh = c.take<uint16_t>((size_t)T * I_s);
   w.nslots = top_k + (I_s > 0 ? 1 : 0);
-  w.slots = c.take<float>((size_t)T * w.nslots * H);
+  w.slots = c.take<int16_t>((size_t)T * w.nslots * H);
+  w.slot_scale = c.take<float>((size_t)T * w.nslots * (H / kSlotBlock));
   return w;
 }
 
@@ -177,6 +179,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   d.K_sh = I_s;
   d.nslab = ceil_div(H, 256);
   d.slots = w.slots;
+  d.slot_scale = w.slot_scale;
   d.nslots = w.nslots;
   d.route_w = route_w;
   d.gamma = gamma;
@@ -193,10 +196,10 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   if (rc) return rc;
   mark(4, stream);
   if (serve)  // the combine folded into the next residual add + norm; `out` is not written
-    rc = launch_combine_add_rmsnorm(w.slots, w.nslots, valid, serve->x_res, serve->norm_w, serve->eps, serve->valid,
-                                    T, H, serve->n_out, stream);
+    rc = launch_combine_add_rmsnorm(w.slots, w.slot_scale, w.nslots, valid, serve->x_res, serve->norm_w, serve->eps,
+                                    serve->valid, T, H, serve->n_out, stream);
   else
-    rc = launch_combine(w.slots, w.nslots, out, T, H, valid, check_ids, top_k, E, stream);
+    rc = launch_combine(w.slots, w.slot_scale, w.nslots, out, T, H, valid, check_ids, top_k, E, stream);
   mark(5, stream);
   return rc;
 }

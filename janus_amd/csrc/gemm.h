@@ -9,11 +9,24 @@ constexpr int kRowBlocks = 6;                 // MFMA row blocks per workgroup t
 constexpr int kChunkRows = 16 * kRowBlocks;   // rows of one expert (or shared-expert tokens) per workgroup
 constexpr int kRowPad = 16;                   // every expert's rows start at a multiple of this in the permuted order
 
+// Slots: each weighted expert output row (one token, one top-k slot; slot top_k is the gated shared expert) is kept
+// as int16 codes with one fp32 scale per block of kSlotBlock columns, value = code * scale. The down epilogue maps
+// the block's largest |value| to code 32767, so a value's error is at most scale / 2 (2^-16 of the block maximum).
+// Within a block the 16 groups of 4 columns are stored in the order the epilogue's lanes hold them: true group g
+// sits at stored group slot_stored_group(g).
+constexpr int kSlotBlock = 64;
+__host__ __device__ inline int slot_stored_group(int g) { return (g & 8) | ((g & 3) << 1) | ((g >> 2) & 1); }
+// The values of one stored group: four int16 codes (two per word, low half first) times the block's scale.
+__device__ __forceinline__ float4 slot_decode4(uint2 v, float scale) {
+  return make_float4((float)(int16_t)(v.x & 0xFFFFu) * scale, (float)((int32_t)v.x >> 16) * scale,
+                     (float)(int16_t)(v.y & 0xFFFFu) * scale, (float)((int32_t)v.y >> 16) * scale);
+}
+
 // One grouped GEMM launch over a chunk list (routed experts) plus, optionally, the shared expert as n_shared_chunks
 // chunks of consecutive tokens.
 //   gate_up: h[row, n] = bf16(silu(x[tok] . Wg[n]) * (x[tok] . Wu[n])) for n < I, W rows 0..I-1 gate, I..2I-1 up.
-//   down:    slots[tok, slot, n] = w(row) * (h[row] . Wd[n]) in fp32, slot = the assignment's top-k slot, or top_k for
-//            the shared expert (weight sigmoid gate). A combine pass sums the slots of each token.
+//   down:    slot (tok, slot) = w(row) * (h[row] . Wd[n]), slot = the assignment's top-k slot, or top_k for the shared
+//            expert (weight sigmoid gate), encoded as above. A combine pass sums the slots of each token.
 struct GemmParams {
   const uint16_t* a;          // gate_up: x [T, K]; down: h of the routed rows [P, K]
   const uint16_t* a_sh;       // down: h of the shared expert [T, K_sh]
@@ -36,7 +49,8 @@ struct GemmParams {
   int nslab;                  // column slabs per chunk
   uint16_t* h;                // gate_up output, routed rows [P, N/2]
   uint16_t* h_sh;             // gate_up output, shared rows [T, N_sh/2]
-  float* slots;               // down output [T, nslots, N]
+  int16_t* slots;             // down output codes [T, nslots, N] (block-permuted columns)
+  float* slot_scale;          // down output scales [T, nslots, N / kSlotBlock]
   int nslots;                 // top_k, plus one when the shared expert runs
   const float* route_w;       // down: routing weight per assignment id [A]
   const float* gamma;         // down: shared-expert weight per token [T], null = 1
@@ -55,10 +69,11 @@ constexpr int kNotFused = 1;  // launch_experts_fused: no persistent kernel for 
 int launch_experts_fused(const GemmParams& gu, const GemmParams& dn, int* sched, int* status, hipStream_t stream);
 int launch_gate_up(const GemmParams& p, hipStream_t stream);
 int launch_down(const GemmParams& p, hipStream_t stream);
-// out[t, n] = bf16(sum_{j < nslots} slots[t, j, n]), summed in slot order in fp32; 0 where valid[t] == 0 (valid null:
-// every token). ids (null: none) are the top-k ids [T, topk]: a slot j < topk whose id is outside [0, E) is skipped.
-int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, const uint8_t* valid,
-                   const int64_t* ids, int topk, int E, hipStream_t stream);
+// out[t, n] = bf16(sum_{j < nslots} slot value (t, j, n)), summed in slot order in fp32; 0 where valid[t] == 0 (valid
+// null: every token). ids (null: none) are the top-k ids [T, topk]: a slot j < topk whose id is outside [0, E) is
+// skipped.
+int launch_combine(const int16_t* slots, const float* slot_scale, int nslots, uint16_t* out, int T, int H,
+                   const uint8_t* valid, const int64_t* ids, int topk, int E, hipStream_t stream);
 int launch_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out, hipStream_t stream);
 int launch_dequant_nvfp4(const uint8_t* q, const uint8_t* s, const float* gs, long rows, int K, uint16_t* out,
                          hipStream_t stream);

@@ -2,8 +2,9 @@
 // accumulation. The semantics are those of the reference's per-tile kernel (janus/moe_w4a16.py:36-86): a tile is one
 // expert times a run of its rows; the gate_up launch fuses silu(gate) * up into its epilogue (:83), the down launch
 // scales by the routing weight (:84-85). Unlike the reference's bf16 y buffer and bf16 reshape-sum (:140), each
-// weighted expert output is kept in fp32 in a per-token slot and a combine pass sums a token's slots in a fixed order
-// and rounds once: the result is deterministic and carries no intermediate bf16 rounding.
+// weighted expert output is kept in a per-token slot as int16 codes with one fp32 scale per 64 columns (16 significant
+// bits against the block's largest value, where bf16 keeps 8 per value), and a combine pass sums a token's slots in
+// fp32 in a fixed order and rounds once: the result is deterministic.
 //
 // Work decomposition. A workgroup (4 waves) takes one chunk (up to 96 rows of one expert, or 96 consecutive tokens of
 // the shared expert) and one column slab. Each wave owns 4 MFMA column blocks of 16 weight rows: it streams their int4
@@ -448,16 +449,43 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
 #pragma unroll
       for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = __builtin_nanf("");
     }
+    // Slot encoding of a row's 64 columns (this wave's block): the 4 lanes of the row (g = 0..3) share the largest
+    // |acc|; code = rint(acc * sign(w) * 32767 / max|acc|), scale = |w| max|acc| / 32767 (NaN with w, for a poisoned
+    // row). fma(v, f, 1.5 * 2^23) rounds v * f to an integer to nearest even and, as |v f| < 2^15 (the reciprocal's
+    // error is far below 0.5 / 32767), leaves its two's complement in the low 16 bits of the result. Lane g stores its
+    // column blocks 0, 1 as stored groups 2g, 2g + 1 and its blocks 2, 3 as 8 + 2g, 9 + 2g (slot_stored_group), so
+    // every store instruction writes 64 contiguous bytes per row. The maxima are taken for every row block before the
+    // first branch: the cross-lane reads need all lanes.
+    float amax[kRowBlocks];
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb) {
+      float a = 0.f;
+#pragma unroll
+      for (int cb = 0; cb < kColBlocks; ++cb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a = fmaxf(a, fabsf(acc[rb][cb][i]));
+      a = fmaxf(a, __shfl_xor(a, 16));
+      amax[rb] = fmaxf(a, __shfl_xor(a, 32));
+    }
+    constexpr float kRound = 12582912.0f;  // 1.5 * 2^23
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
       const int m = rb * 16 + nl;
       if (rb >= nrb || m >= rows) continue;
-      float* orow = p.slots + orow_off[rb] + col0 + 4 * g;
       const float w = wt[rb];
+      const float f0 = amax[rb] > 0.f ? 32767.0f * __builtin_amdgcn_rcpf(amax[rb]) : 0.f;
+      const float f = w < 0.f ? -f0 : f0;
+      uint32_t code[2 * kColBlocks];
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb)
-        *reinterpret_cast<float4*>(orow + 16 * cb) =
-            make_float4(w * acc[rb][cb][0], w * acc[rb][cb][1], w * acc[rb][cb][2], w * acc[rb][cb][3]);
+#pragma unroll
+        for (int i = 0; i < 4; i += 2)
+          code[2 * cb + i / 2] = __builtin_amdgcn_perm(__float_as_uint(fmaf(acc[rb][cb][i + 1], f, kRound)),
+                                                       __float_as_uint(fmaf(acc[rb][cb][i], f, kRound)), 0x05040100u);
+      int16_t* orow = p.slots + orow_off[rb] + col0;
+      *reinterpret_cast<uint4*>(orow + 8 * g) = make_uint4(code[0], code[1], code[2], code[3]);
+      *reinterpret_cast<uint4*>(orow + 32 + 8 * g) = make_uint4(code[4], code[5], code[6], code[7]);
+      if (g == 0) p.slot_scale[(orow_off[rb] + col0) / kSlotBlock] = fabsf(w) * amax[rb] * (1.0f / 32767.0f);
     }
   }
 }
@@ -556,15 +584,19 @@ __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmPara
   }
 }
 
-// out[t, n] = bf16(sum_j slots[t, j, n]), four columns per thread, slots summed in order. The loads of up to 8 slots
-// are issued together before the additions. A padding token (valid[t] == 0) gets zeros and its slots are not read.
-// With ids (the caller's top-k ids [T, topk], int64), slot j < topk of token t counts only when its id is in [0, E):
-// the GEMMs never write the slot of a dropped assignment, so it is skipped (the load still issues, its value unused).
+// out[t, n] = bf16(sum_j slot value (t, j, n)), four columns (one group) per thread, slots summed in order in fp32.
+// The codes and scales of up to 8 slots are loaded together before the additions. A padding token (valid[t] == 0)
+// gets zeros and its slots are not read. With ids (the caller's top-k ids [T, topk], int64), slot j < topk of token t
+// counts only when its id is in [0, E): the GEMMs never write the slot of a dropped assignment, so it is skipped (the
+// loads still issue, their values unused).
 template <bool kIds>
-__global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uint2* __restrict__ out, int T, int H4,
-                               const uint8_t* __restrict__ valid, const int64_t* __restrict__ ids, int topk, int E) {
+__global__ void combine_kernel(const uint2* __restrict__ slots, const float* __restrict__ scales, int nslots,
+                               uint2* __restrict__ out, int T, int H4, const uint8_t* __restrict__ valid,
+                               const int64_t* __restrict__ ids, int topk, int E) {
   constexpr int kBatch = 8;
+  constexpr int kGroups = kSlotBlock / 4;  // groups of 4 columns per scale block
   const long n = (long)T * H4;
+  const int nblk = H4 / kGroups;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
     const long t = i / H4, col = i - t * H4;
     if (valid && !valid[t]) {
@@ -578,22 +610,29 @@ __global__ void combine_kernel(const float4* __restrict__ slots, int nslots, uin
         if (e < 0 || e >= E) keep &= ~(1u << j);
       }
     }
-    const float4* src = slots + t * nslots * H4 + col;
-    float4 s = src[0];
+    const uint2* src = slots + t * nslots * H4 + (col & ~(long)(kGroups - 1)) + slot_stored_group((int)col % kGroups);
+    const float* ssrc = scales + t * nslots * nblk + col / kGroups;
+    float4 s = slot_decode4(src[0], ssrc[0]);
     if (kIds && !(keep & 1u)) s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j0 = 1; j0 < nslots; j0 += kBatch) {
-      f32x4 v[kBatch];
+      uint2 v[kBatch];
+      float sc[kBatch];
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        if (j0 + j < nslots)
-          v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + (long)(j0 + j) * H4));
+      for (int j = 0; j < kBatch; ++j) {
+        if (j0 + j < nslots) {
+          const u32x2 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + (long)(j0 + j) * H4));
+          v[j] = make_uint2(raw[0], raw[1]);
+          sc[j] = ssrc[(long)(j0 + j) * nblk];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
         if (j0 + j < nslots && (!kIds || ((keep >> (j0 + j)) & 1u))) {
-          s.x += v[j][0];
-          s.y += v[j][1];
-          s.z += v[j][2];
-          s.w += v[j][3];
+          const float4 d = slot_decode4(v[j], sc[j]);
+          s.x += d.x;
+          s.y += d.y;
+          s.z += d.z;
+          s.w += d.w;
         }
       }
     }
@@ -723,22 +762,23 @@ int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* 
 int launch_gate_up(const GemmParams& p, hipStream_t stream) { return launch_gemm<kGateUp>(p, stream); }
 int launch_down(const GemmParams& p, hipStream_t stream) { return launch_gemm<kDown>(p, stream); }
 
-int launch_combine(const float* slots, int nslots, uint16_t* out, int T, int H, const uint8_t* valid,
-                   const int64_t* ids, int topk, int E, hipStream_t stream) {
+int launch_combine(const int16_t* slots, const float* slot_scale, int nslots, uint16_t* out, int T, int H,
+                   const uint8_t* valid, const int64_t* ids, int topk, int E, hipStream_t stream) {
   const long n4 = (long)T * (H / 4);
   if (n4 == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(H % kSlotBlock == 0, JANUS_MOE_EINVAL, "combine: H=%d is not a multiple of %d", H, kSlotBlock);
   JANUS_REQUIRE(!ids || (topk > 0 && topk <= 32), JANUS_MOE_EINVAL, "combine: top_k=%d with id checks (at most 32)",
                 topk);
   long blocks = (n4 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   if (ids)
     hipLaunchKernelGGL(combine_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       reinterpret_cast<const float4*>(slots), nslots, reinterpret_cast<uint2*>(out), T, H / 4, valid,
-                       ids, topk, E);
+                       reinterpret_cast<const uint2*>(slots), slot_scale, nslots, reinterpret_cast<uint2*>(out), T,
+                       H / 4, valid, ids, topk, E);
   else
     hipLaunchKernelGGL(combine_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       reinterpret_cast<const float4*>(slots), nslots, reinterpret_cast<uint2*>(out), T, H / 4, valid,
-                       nullptr, 0, 0);
+                       reinterpret_cast<const uint2*>(slots), slot_scale, nslots, reinterpret_cast<uint2*>(out), T,
+                       H / 4, valid, nullptr, 0, 0);
   JANUS_LAUNCH_CHECK("combine");
   return JANUS_MOE_OK;
 }

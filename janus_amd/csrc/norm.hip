@@ -9,6 +9,7 @@
 // (fp32 slot) access; the sum of squares is reduced in a fixed lane order, so the standalone kernel and the fused
 // combine give the same bits.
 #include "norm.h"
+#include "gemm.h"
 
 namespace janus {
 namespace {
@@ -108,8 +109,9 @@ __global__ void __launch_bounds__(kNormWaves * kWave) add_rmsnorm_kernel(
 // columns, whose registers would not allow two waves per SIMD otherwise).
 template <int NV>
 __global__ void __launch_bounds__(kNormWaves * kWave) combine_add_rmsnorm_kernel(
-    const float4* __restrict__ slots, int nslots, const uint8_t* __restrict__ moe_valid, uint16_t* x_res,
-    const uint16_t* __restrict__ w, float eps, const uint8_t* __restrict__ valid, int T, int H, uint16_t* n_out) {
+    const uint2* __restrict__ slots, const float* __restrict__ scales, int nslots,
+    const uint8_t* __restrict__ moe_valid, uint16_t* x_res, const uint16_t* __restrict__ w, float eps,
+    const uint8_t* __restrict__ valid, int T, int H, uint16_t* n_out) {
   const int lane = threadIdx.x & (kWave - 1);
   const long t = (long)blockIdx.x * kNormWaves + threadIdx.x / kWave;
   if (t >= T) return;
@@ -127,27 +129,36 @@ __global__ void __launch_bounds__(kNormWaves * kWave) combine_add_rmsnorm_kernel
 #pragma unroll
   for (int j = 0; j < NV; ++j) s[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (routed) {
-    const float4* src = slots + t * nslots * ncol4 + lane;
+    // the lane's column group c4 = lane + 64 j sits at its stored position within its scale block
+    constexpr int kGroups = kSlotBlock / 4;
+    const int nblk = ncol4 / kGroups;
+    const long row0 = t * nslots;
+    const int q = (lane & ~(kGroups - 1)) | slot_stored_group(lane & (kGroups - 1));
     for (int k0 = 0; k0 < nslots; k0 += kSlotBatch) {
-      float4 a[kSlotBatch][NV];
+      uint2 a[kSlotBatch][NV];
+      float sc[kSlotBatch][NV];
 #pragma unroll
       for (int kk = 0; kk < kSlotBatch; ++kk)
 #pragma unroll
         for (int j = 0; j < NV; ++j)
-          if (k0 + kk < nslots && lane + kWave * j < ncol4) a[kk][j] = src[(long)(k0 + kk) * ncol4 + kWave * j];
+          if (k0 + kk < nslots && lane + kWave * j < ncol4) {
+            a[kk][j] = slots[(row0 + k0 + kk) * ncol4 + kWave * j + q];
+            sc[kk][j] = scales[(row0 + k0 + kk) * nblk + (lane + kWave * j) / kGroups];
+          }
 #pragma unroll
       for (int kk = 0; kk < kSlotBatch; ++kk) {
         if (k0 + kk >= nslots) break;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
           if (lane + kWave * j >= ncol4) continue;
+          const float4 d = slot_decode4(a[kk][j], sc[kk][j]);
           if (k0 + kk == 0) {
-            s[j] = a[kk][j];  // slot 0 starts the sum, as in the plain combine
+            s[j] = d;  // slot 0 starts the sum, as in the plain combine
           } else {
-            s[j].x += a[kk][j].x;
-            s[j].y += a[kk][j].y;
-            s[j].z += a[kk][j].z;
-            s[j].w += a[kk][j].w;
+            s[j].x += d.x;
+            s[j].y += d.y;
+            s[j].z += d.z;
+            s[j].w += d.w;
           }
         }
       }
@@ -201,13 +212,15 @@ int launch_add_rmsnorm(const uint16_t* residual, const uint16_t* h, const uint16
   return JANUS_MOE_OK;
 }
 
-int launch_combine_add_rmsnorm(const float* slots, int nslots, const uint8_t* moe_valid, uint16_t* x_res,
-                               const uint16_t* w, float eps, const uint8_t* valid, int T, int H, uint16_t* n_out,
-                               hipStream_t stream) {
+int launch_combine_add_rmsnorm(const int16_t* slots, const float* slot_scale, int nslots, const uint8_t* moe_valid,
+                               uint16_t* x_res, const uint16_t* w, float eps, const uint8_t* valid, int T, int H,
+                               uint16_t* n_out, hipStream_t stream) {
   if (T == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(H % kSlotBlock == 0, JANUS_MOE_EINVAL, "combine_add_rmsnorm: H=%d is not a multiple of %d", H,
+                kSlotBlock);
   const dim3 g(ceil_div(T, kNormWaves)), b(kNormWaves * kWave);
-  JANUS_NORM_CASES(combine_add_rmsnorm_kernel, reinterpret_cast<const float4*>(slots), nslots, moe_valid, x_res, w,
-                   eps, valid, T, H, n_out)
+  JANUS_NORM_CASES(combine_add_rmsnorm_kernel, reinterpret_cast<const uint2*>(slots), slot_scale, nslots, moe_valid,
+                   x_res, w, eps, valid, T, H, n_out)
   JANUS_LAUNCH_CHECK("combine_add_rmsnorm");
   return JANUS_MOE_OK;
 }
