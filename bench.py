@@ -146,7 +146,9 @@ def variant_timings(cfg, x, blk, dev) -> dict:
       - serve_unfused / serve_fused: _add_norm, the layer and the next _add_norm as three calls, and as one call whose
         combine writes the second _add_norm;
       - experts_int4 / experts_nvfp4: fused_moe on the layer's routing with the int4 stacks and with NVFP4 stacks of
-        the same shape (random weights quantised on the GPU).
+        the same shape (random weights quantised on the GPU);
+      - block_nvfp4: the whole layer (router, routed and shared experts) with the same layer's weights re-encoded in
+        NVFP4 (synth.nvfp4_layer, quantised on the GPU), one block_forward_nvfp4 call.
     Each entry that fails is reported as its error text instead."""
     from janus_amd import ops
     from janus_amd.hybrid import nvfp4_quantize
@@ -195,6 +197,15 @@ def variant_timings(cfg, x, blk, dev) -> dict:
         del gu, gus, gug, dn, dns, dng
     except Exception as exc:
         out["experts_nvfp4"] = f"{type(exc).__name__}: {exc}"[:200]
+    try:
+        from janus_amd import synth
+        from janus_amd.block import NVFP4SparseMoeBlock
+
+        nv = NVFP4SparseMoeBlock.from_tensors(synth.nvfp4_layer(cfg, device=dev), cfg.k)
+        run("block_nvfp4", lambda: nv(x))
+        del nv
+    except Exception as exc:
+        out["block_nvfp4"] = f"{type(exc).__name__}: {exc}"[:200]
     return out
 
 

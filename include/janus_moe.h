@@ -182,6 +182,38 @@ JANUS_MOE_API int janus_moe_block_forward_masked(const janus_moe_block_weights* 
                                                  float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------
+ * The same block with the checkpoint's own NVFP4 weights, the layer load_nvfp4 builds (janus/hybrid.py:1462-1475):
+ * routed experts as NVFP4Experts stacks (janus/hybrid.py:512-572) and the shared expert's gate_proj / up_proj /
+ * down_proj as NVFP4Linear (:483-509), decoded inside the GEMMs as janus_moe_experts_nvfp4 does; router, shared gate,
+ * valid mask, outputs and workspace (janus_moe_block_workspace_bytes) as in janus_moe_block_forward_masked. The
+ * shared expert's gate and up weights are stacked like the routed ones (gate rows first), each row with its own fp32
+ * global scale (a linear's weight_scale_2 repeated over its rows). */
+typedef struct janus_moe_block_weights_nvfp4 {
+  int H, I, E, top_k;             /* hidden, routed intermediate, experts, experts per token */
+  int I_s;                        /* shared-expert intermediate; 0 = no shared expert */
+  const float* router_w;          /* [E, H] fp32 */
+  const void* router_prep;        /* janus_moe_router_prepare(router_w) */
+  const float* router_bias;       /* [E] fp32 or NULL */
+  const uint8_t* gate_up;         /* [E, 2I, H/2] e2m1 pairs */
+  const uint8_t* gate_up_scale;   /* [E, 2I, H/16] e4m3 */
+  const float* gate_up_global;    /* [E, 2I] fp32 */
+  const uint8_t* down;            /* [E, H, I/2] */
+  const uint8_t* down_scale;      /* [E, H, I/16] */
+  const float* down_global;       /* [E, H] */
+  const uint8_t* sh_gate_up;      /* [2 I_s, H/2] */
+  const uint8_t* sh_gate_up_scale;/* [2 I_s, H/16] */
+  const float* sh_gate_up_global; /* [2 I_s] */
+  const uint8_t* sh_down;         /* [H, I_s/2] */
+  const uint8_t* sh_down_scale;   /* [H, I_s/16] */
+  const float* sh_down_global;    /* [H] */
+  const uint16_t* sh_gate_w;      /* [H] bf16 (shared_expert_gate.weight) */
+} janus_moe_block_weights_nvfp4;
+
+JANUS_MOE_API int janus_moe_block_forward_nvfp4(const janus_moe_block_weights_nvfp4* w, const uint16_t* x,
+                                                const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                                float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
  * janus_moe_block_forward_masked without a workspace argument. No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Its scratch is a static device array of JANUS_MOE_NOALLOC_SCRATCH_BYTES per GPU (64 MiB, held until

@@ -23,7 +23,7 @@ EXPORTS = (
     "janus_moe_add_rmsnorm", "janus_moe_block_forward_serve",
     "janus_moe_dequant", "janus_moe_profile_events",
     "janus_moe_experts_nvfp4", "janus_moe_dequant_nvfp4", "janus_moe_device_status",
-    "janus_moe_block_forward_noalloc",
+    "janus_moe_block_forward_noalloc", "janus_moe_block_forward_nvfp4",
 )
 
 _p, _i, _z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -36,6 +36,19 @@ class BlockWeights(ctypes.Structure):
         ("router_w", _p), ("router_prep", _p), ("router_bias", _p),
         ("gate_up_q", _p), ("gate_up_s", _p), ("down_q", _p), ("down_s", _p),
         ("sh_gate_up_q", _p), ("sh_gate_up_s", _p), ("sh_down_q", _p), ("sh_down_s", _p),
+        ("sh_gate_w", _p),
+    ]
+
+
+class BlockWeightsNvfp4(ctypes.Structure):
+    """janus_moe_block_weights_nvfp4."""
+    _fields_ = [
+        ("H", _i), ("I", _i), ("E", _i), ("top_k", _i), ("I_s", _i),
+        ("router_w", _p), ("router_prep", _p), ("router_bias", _p),
+        ("gate_up", _p), ("gate_up_scale", _p), ("gate_up_global", _p),
+        ("down", _p), ("down_scale", _p), ("down_global", _p),
+        ("sh_gate_up", _p), ("sh_gate_up_scale", _p), ("sh_gate_up_global", _p),
+        ("sh_down", _p), ("sh_down_scale", _p), ("sh_down_global", _p),
         ("sh_gate_w", _p),
     ]
 
@@ -63,6 +76,7 @@ _SIGNATURES = {
     "janus_moe_dequant_nvfp4": (_i, [_p, _p, _p, ctypes.c_long, _i, _p, _p]),
     "janus_moe_device_status": (_i, [_p, _i, _p]),
     "janus_moe_block_forward_noalloc": (_i, [ctypes.POINTER(BlockWeights), _p, _p, _i, _p, _p, _p, _p]),
+    "janus_moe_block_forward_nvfp4": (_i, [ctypes.POINTER(BlockWeightsNvfp4), _p, _p, _i, _p, _p, _p, _p, _z, _p]),
 }
 
 _handle = None

@@ -14,20 +14,25 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import ops
-from .hybrid import W4A16Experts, W4A16Linear, moe_kernel
+from .hybrid import NVFP4Experts, NVFP4Linear, W4A16Experts, W4A16Linear, moe_kernel
 
 
 class W4A16TopKRouter(nn.Module):
     """Qwen3_5MoeTopKRouter: weight [E, H] fp32, forward(h) -> (router_logits [T, E] fp32, scores [T, k], indices
     [T, k] int64). On the GPU the selection is the exact rule of the route op: the k largest correctly rounded fp32
     logits, ties to the lower expert id, slots in descending order; scores are the softmax renormalised over the top-k.
-    `bias` (optional [E] fp32) is added to the logits before selection."""
+    `bias` (optional [E] fp32) is added to the logits before selection.
+
+    Under inference on a GPU router_logits is None unless `return_logits` is set: the HF MoE block discards it
+    (`_, routing_weights, selected_experts = self.gate(...)`), and the route op does not need the dense fp32 logits
+    GEMM, so it is only run for a caller that records router logits."""
 
     def __init__(self, weight: torch.Tensor, top_k: int, bias: torch.Tensor | None = None):
         super().__init__()
         self.weight = nn.Parameter(weight.float(), requires_grad=False)
         self.register_buffer("bias", None if bias is None else bias.float(), persistent=False)
         self.top_k, self.num_experts, self.hidden_dim = top_k, weight.shape[0], weight.shape[1]
+        self.return_logits = False
         self._prep, self._prep_key = None, None
 
     def prep(self) -> torch.Tensor:
@@ -50,15 +55,17 @@ class W4A16TopKRouter(nn.Module):
             self.prep()  # eagerly, so that a capture that is the first forward finds it ready
         return self
 
+    def logits(self, x):
+        out = F.linear(x.float(), self.weight)
+        return out if self.bias is None else out + self.bias
+
     def forward(self, hidden_states):
         x = hidden_states.reshape(-1, self.hidden_dim)
-        logits = F.linear(x.float(), self.weight)
-        if self.bias is not None:
-            logits = logits + self.bias
         if x.is_cuda and not torch.is_grad_enabled():
             idx, w, _ = ops.route(x.to(torch.bfloat16).contiguous(), self.weight, self.prep(), self.bias, None,
                                   self.top_k)
-            return logits, w, idx.long()
+            return (self.logits(x) if self.return_logits else None), w, idx.long()
+        logits = self.logits(x)
         probs = torch.softmax(logits, dim=-1, dtype=torch.float)
         top, idx = torch.topk(probs, self.top_k, dim=-1)
         top = top / top.sum(dim=-1, keepdim=True)
@@ -120,15 +127,7 @@ class W4A16SparseMoeBlock(nn.Module):
         if keep is not None and keep.shape[0] != x.shape[0]:
             raise ValueError(f"valid has {keep.shape[0]} entries for {x.shape[0]} tokens")
         if x.is_cuda and not torch.is_grad_enabled() and moe_kernel(x.device) == "fused":
-            sh = self.shared_expert
-            out, _, _ = ops.block_forward(
-                x.to(torch.bfloat16).contiguous(), self.gate.weight, self.gate.prep(), self.gate.bias,
-                self.experts.gate_up, self.experts.gate_up_scale, self.experts.down, self.experts.down_scale,
-                None if sh is None else sh.gate_up, None if sh is None else sh.gate_up_scale,
-                None if sh is None else sh.down, None if sh is None else sh.down_scale,
-                None if self.shared_expert_gate is None else
-                self.shared_expert_gate.weight.reshape(-1).to(torch.bfloat16).contiguous(),
-                self.gate.top_k, None if keep is None else keep.to(torch.bool).contiguous())
+            out = self._fused(x.to(torch.bfloat16).contiguous(), None if keep is None else keep.to(torch.bool).contiguous())
             return out.to(hidden_states.dtype).reshape(shape)
         _, weights, idx = self.gate(x)
         out = self.experts(x, idx, weights.to(x.dtype))
@@ -141,6 +140,23 @@ class W4A16SparseMoeBlock(nn.Module):
             out = torch.where(keep.to(out.device, torch.bool)[:, None], out, torch.zeros_like(out))
         return out.reshape(shape)
 
+    def _shared_gate_w(self):
+        g = self.shared_expert_gate
+        return None if g is None else g.weight.reshape(-1).to(torch.bfloat16).contiguous()
+
+    def _fused(self, x, keep):
+        """The whole block as one janus_moe::block_forward call: x [T, H] bf16, keep [T] bool or None."""
+        sh = self.shared_expert
+        out, _, _ = ops.block_forward(
+            x, self.gate.weight, self.gate.prep(), self.gate.bias,
+            self.experts.gate_up, self.experts.gate_up_scale, self.experts.down, self.experts.down_scale,
+            None if sh is None else sh.gate_up, None if sh is None else sh.gate_up_scale,
+            None if sh is None else sh.down, None if sh is None else sh.down_scale,
+            self._shared_gate_w(), self.gate.top_k, keep)
+        return out
+
+    _fused_serve = True  # the serving entry (block_forward_serve) takes this codec
+
     def serve(self, x, h_attn, post_norm, next_norm, valid=None, next_valid=None):
         """The layer between its serving neighbours (janus/hybrid.py:1096-1105, `_serve_level`):
             x1, n1 = _add_norm(x, h_attn, post_norm); moe = self(n1, valid); return _add_norm(x1, moe, next_norm,
@@ -152,7 +168,8 @@ class W4A16SparseMoeBlock(nn.Module):
         shape = x.shape
         flat = lambda t: None if t is None else t.reshape(-1, shape[-1])
         mask = lambda m: None if m is None else m.reshape(-1).to(torch.bool).contiguous()
-        if x.is_cuda and not torch.is_grad_enabled() and moe_kernel(x.device) == "fused" and x.dtype == torch.bfloat16:
+        if (self._fused_serve and x.is_cuda and not torch.is_grad_enabled() and moe_kernel(x.device) == "fused"
+                and x.dtype == torch.bfloat16):
             sh = self.shared_expert
             x_out, h_out = ops.block_forward_serve(
                 flat(x).contiguous(), None if h_attn is None else flat(h_attn).contiguous(),
@@ -172,3 +189,79 @@ class W4A16SparseMoeBlock(nn.Module):
         if next_valid is not None:
             h = torch.where(next_valid.reshape(*shape[:-1], 1).to(h.device, torch.bool), h, torch.zeros_like(h))
         return x2, h
+
+
+class NVFP4MLP(nn.Module):
+    """Qwen3_5MoeMLP with NVFP4Linear projections, as load_nvfp4 leaves the shared expert."""
+
+    def __init__(self, gate_proj: NVFP4Linear, up_proj: NVFP4Linear, down_proj: NVFP4Linear, act_fn=F.silu):
+        super().__init__()
+        self.gate_proj, self.up_proj, self.down_proj, self.act_fn = gate_proj, up_proj, down_proj, act_fn
+
+    def forward(self, x):
+        return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+
+
+class NVFP4SparseMoeBlock(W4A16SparseMoeBlock):
+    """The block as `load_nvfp4` leaves it (janus/hybrid.py:1462-1475): routed experts `NVFP4Experts`, the shared
+    expert's gate_proj / up_proj / down_proj `NVFP4Linear` (janus/hybrid.py:483-509). Under inference on a GPU
+    forward is one `janus_moe::block_forward_nvfp4` call (router, routed and shared experts decoded inside the HIP
+    GEMMs, one fp32 sum rounded once); otherwise the HF composition of the submodules. The shared expert's packed
+    weights are stacked once here, gate rows first, each row carrying its linear's global scale."""
+
+    _fused_serve = False  # the serving entry takes int4 weights: serve() composes its parts
+
+    def __init__(self, gate: W4A16TopKRouter, experts: NVFP4Experts, shared_expert: nn.Module | None,
+                 shared_expert_gate: nn.Linear | None):
+        super().__init__(gate, experts, shared_expert, shared_expert_gate)
+        stacked = {}
+        if shared_expert is not None:
+            gp, up, dp = shared_expert.gate_proj, shared_expert.up_proj, shared_expert.down_proj
+            if not all(isinstance(m, NVFP4Linear) for m in (gp, up, dp)):
+                raise TypeError("NVFP4SparseMoeBlock: the shared expert's projections must be NVFP4Linear")
+            I_s = gp.out_features
+            stacked = dict(
+                sh_gate_up=torch.cat([gp.packed, up.packed]), sh_gate_up_scale=torch.cat([gp.scale, up.scale]),
+                sh_gate_up_global=torch.cat([gp.global_scale.reshape(1).expand(I_s),
+                                             up.global_scale.reshape(1).expand(I_s)]).float(),
+                sh_down=dp.packed, sh_down_scale=dp.scale,
+                sh_down_global=dp.global_scale.reshape(1).expand(dp.out_features).float().contiguous())
+        for name in ("sh_gate_up", "sh_gate_up_scale", "sh_gate_up_global", "sh_down", "sh_down_scale",
+                     "sh_down_global"):
+            self.register_buffer(name, stacked.get(name), persistent=False)
+
+    @classmethod
+    def from_tensors(cls, w: dict, top_k: int, dtype=torch.bfloat16) -> "NVFP4SparseMoeBlock":
+        """Builds the block from a `janus_amd.synth.nvfp4_layer` dict (per-row globals constant per projection)."""
+        router = W4A16TopKRouter(w["router_w"], top_k, w.get("router_bias"))
+        col = lambda t: t.reshape(*t.shape, 1)
+        experts = NVFP4Experts(w["gate_up"], w["gate_up_scale"], col(w["gate_up_global"]), w["down"], w["down_scale"],
+                               col(w["down_global"]))
+        shared, shared_gate = None, None
+        if w.get("sh_gate_up") is not None:
+            I_s = w["sh_gate_up"].shape[0] // 2
+            lin = lambda p, s, g: NVFP4Linear(p, s, g[0])
+            shared = NVFP4MLP(lin(w["sh_gate_up"][:I_s], w["sh_gate_up_scale"][:I_s], w["sh_gate_up_global"][:I_s]),
+                              lin(w["sh_gate_up"][I_s:], w["sh_gate_up_scale"][I_s:], w["sh_gate_up_global"][I_s:]),
+                              lin(w["sh_down"], w["sh_down_scale"], w["sh_down_global"]))
+            H = w["router_w"].shape[1]
+            shared_gate = nn.Linear(H, 1, bias=False, dtype=dtype, device=w["router_w"].device)
+            with torch.no_grad():
+                shared_gate.weight.copy_(w["sh_gate_w"].reshape(1, H).to(dtype))
+            shared_gate.weight.requires_grad_(False)
+        return cls(router, experts, shared, shared_gate)
+
+    @classmethod
+    def from_module(cls, mlp: nn.Module) -> "NVFP4SparseMoeBlock":
+        """Wraps a loaded Qwen3_5MoeSparseMoeBlock (`gate` with `weight` and `top_k`, `experts` NVFP4Experts,
+        `shared_expert`, `shared_expert_gate`); the router weight is shared, not copied."""
+        gate = W4A16TopKRouter(mlp.gate.weight.detach(), mlp.gate.top_k, getattr(mlp.gate, "bias", None))
+        return cls(gate, mlp.experts, getattr(mlp, "shared_expert", None), getattr(mlp, "shared_expert_gate", None))
+
+    def _fused(self, x, keep):
+        ex = self.experts
+        out, _, _ = ops.block_forward_nvfp4(
+            x, self.gate.weight, self.gate.prep(), self.gate.bias, ex.gate_up, ex.gate_up_scale, ex.gate_up_global,
+            ex.down, ex.down_scale, ex.down_global, self.sh_gate_up, self.sh_gate_up_scale, self.sh_gate_up_global,
+            self.sh_down, self.sh_down_scale, self.sh_down_global, self._shared_gate_w(), self.gate.top_k, keep)
+        return out

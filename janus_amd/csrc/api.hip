@@ -126,7 +126,8 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
                 const uint16_t* sds, const float* gamma, int T, int H, int I, int I_s, int E, int top_k, uint16_t* out,
                 const ExpertsWorkspace& w, hipStream_t stream, int codec = 0, const float* gu_global = nullptr,
                 const float* dn_global = nullptr, const uint8_t* valid = nullptr,
-                const ServeEpilogue* serve = nullptr, const int64_t* check_ids = nullptr) {
+                const ServeEpilogue* serve = nullptr, const int64_t* check_ids = nullptr,
+                const float* sgu_global = nullptr, const float* sdn_global = nullptr) {
   const int A = T * top_k;
   int* status = device_status_word();
   JANUS_REQUIRE(status, JANUS_MOE_ELAUNCH, "the device status word of this library could not be resolved");
@@ -157,6 +158,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.K = H;
   p.q_sh = sguq;
   p.s_sh = sgus;
+  p.gsc_sh = sgu_global;
   p.N_sh = 2 * I_s;
   p.K_sh = H;
   p.nslab = ceil_div(I > I_s ? I : I_s, 128);
@@ -175,6 +177,7 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   d.K = I;
   d.q_sh = sdq;
   d.s_sh = sds;
+  d.gsc_sh = sdn_global;
   d.N_sh = H;
   d.K_sh = I_s;
   d.nslab = ceil_div(H, 256);
@@ -322,12 +325,39 @@ extern "C" int janus_moe_block_forward(const janus_moe_block_weights* wt, const 
 }
 
 namespace {
-// The block forward behind the three block entries: x is the MoE input; serve null writes the layer output to out.
-int block_forward(const janus_moe_block_weights* wt, const uint16_t* x, const uint8_t* valid, int T, uint16_t* out,
+// Either codec's block weights, as the pipeline reads them: weight and scale pointers untyped (int4 words and bf16
+// scales, or NVFP4 bytes and e4m3 scales), plus the NVFP4 global scales per weight row (null for int4).
+struct BlockView {
+  int H, I, E, top_k, I_s, codec;
+  const float* router_w;
+  const void* router_prep;
+  const float* router_bias;
+  const void *gate_up, *gate_up_scale, *down, *down_scale;
+  const float *gate_up_global, *down_global;
+  const void *sh_gate_up, *sh_gate_up_scale, *sh_down, *sh_down_scale;
+  const float *sh_gate_up_global, *sh_down_global;
+  const uint16_t* sh_gate_w;
+};
+
+BlockView view_of(const janus_moe_block_weights* w) {
+  return BlockView{w->H, w->I, w->E, w->top_k, w->I_s, 0, w->router_w, w->router_prep, w->router_bias,
+                   w->gate_up_q, w->gate_up_s, w->down_q, w->down_s, nullptr, nullptr,
+                   w->sh_gate_up_q, w->sh_gate_up_s, w->sh_down_q, w->sh_down_s, nullptr, nullptr, w->sh_gate_w};
+}
+
+BlockView view_of(const janus_moe_block_weights_nvfp4* w) {
+  return BlockView{w->H, w->I, w->E, w->top_k, w->I_s, 1, w->router_w, w->router_prep, w->router_bias,
+                   w->gate_up, w->gate_up_scale, w->down, w->down_scale, w->gate_up_global, w->down_global,
+                   w->sh_gate_up, w->sh_gate_up_scale, w->sh_down, w->sh_down_scale, w->sh_gate_up_global,
+                   w->sh_down_global, w->sh_gate_w};
+}
+
+// The block forward behind the block entries: x is the MoE input; serve null writes the layer output to out.
+int block_forward(const BlockView* wt, const uint16_t* x, const uint8_t* valid, int T, uint16_t* out,
                   int32_t* topk_idx, float* topk_w, void* ws, size_t ws_bytes, hipStream_t stream,
                   const ServeEpilogue* serve) {
-  JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward: null weights");
   const int H = wt->H, I = wt->I, E = wt->E, k = wt->top_k, I_s = wt->I_s;
+  const bool nv = wt->codec == 1;
   int rc = check_expert_sizes("janus_moe_block_forward", T, H, I, E, k, I_s > 0 ? I_s : 0);
   if (rc) return rc;
   rc = check_route_sizes(T, H, E, k);
@@ -335,10 +365,11 @@ int block_forward(const janus_moe_block_weights* wt, const uint16_t* x, const ui
   JANUS_REQUIRE(I_s >= 0 && I_s % 128 == 0, JANUS_MOE_EINVAL, "janus_moe_block_forward: I_s=%d must be a multiple of 128",
                 I_s);
   if (T == 0) return JANUS_MOE_OK;
-  JANUS_REQUIRE(x && (out || serve) && wt->router_w && wt->router_prep && wt->gate_up_q && wt->gate_up_s &&
-                    wt->down_q && wt->down_s &&
-                    (I_s == 0 || (wt->sh_gate_up_q && wt->sh_gate_up_s && wt->sh_down_q && wt->sh_down_s)),
-                JANUS_MOE_EINVAL, "janus_moe_block_forward: null pointer");
+  JANUS_REQUIRE(x && (out || serve) && wt->router_w && wt->router_prep && wt->gate_up && wt->gate_up_scale &&
+                    wt->down && wt->down_scale && (!nv || (wt->gate_up_global && wt->down_global)) &&
+                    (I_s == 0 || (wt->sh_gate_up && wt->sh_gate_up_scale && wt->sh_down && wt->sh_down_scale &&
+                                  (!nv || (wt->sh_gate_up_global && wt->sh_down_global)))),
+                JANUS_MOE_EINVAL, "janus_moe_block_forward%s: null pointer", nv ? "_nvfp4" : "");
   const size_t need = janus_moe_block_workspace_bytes(T, H, I, E, k, I_s);
   JANUS_REQUIRE(ws && ws_bytes >= need, JANUS_MOE_EWORKSPACE, "janus_moe_block_forward: workspace %zu < %zu bytes",
                 ws_bytes, need);
@@ -351,16 +382,30 @@ int block_forward(const janus_moe_block_weights* wt, const uint16_t* x, const ui
   rc = launch_route(x, wt->router_w, wt->router_prep, wt->router_bias, gated ? wt->sh_gate_w : nullptr, T, H, E, k,
                     valid, idx, rw, b.gamma, b.route, stream);
   if (rc) return rc;
-  return run_experts<int>(x, idx, rw, wt->gate_up_q, wt->gate_up_s, wt->down_q, wt->down_s, wt->sh_gate_up_q,
-                          wt->sh_gate_up_s, wt->sh_down_q, wt->sh_down_s, gated ? b.gamma : nullptr, T, H, I, I_s, E, k,
-                          out, b.experts, stream, 0, nullptr, nullptr, valid, serve);
+  auto words = [](const void* p) { return static_cast<const int32_t*>(p); };
+  auto halves = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  return run_experts<int>(x, idx, rw, words(wt->gate_up), halves(wt->gate_up_scale), words(wt->down),
+                          halves(wt->down_scale), words(wt->sh_gate_up), halves(wt->sh_gate_up_scale),
+                          words(wt->sh_down), halves(wt->sh_down_scale), gated ? b.gamma : nullptr, T, H, I, I_s, E, k,
+                          out, b.experts, stream, wt->codec, wt->gate_up_global, wt->down_global, valid, serve,
+                          nullptr, wt->sh_gate_up_global, wt->sh_down_global);
 }
 }  // namespace
 
 extern "C" int janus_moe_block_forward_masked(const janus_moe_block_weights* wt, const uint16_t* x,
                                               const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
                                               float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream) {
-  return block_forward(wt, x, valid, T, out, topk_idx, topk_w, ws, ws_bytes, (hipStream_t)stream, nullptr);
+  JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward: null weights");
+  const BlockView v = view_of(wt);
+  return block_forward(&v, x, valid, T, out, topk_idx, topk_w, ws, ws_bytes, (hipStream_t)stream, nullptr);
+}
+
+extern "C" int janus_moe_block_forward_nvfp4(const janus_moe_block_weights_nvfp4* wt, const uint16_t* x,
+                                             const uint8_t* valid, int T, uint16_t* out, int32_t* topk_idx,
+                                             float* topk_w, void* ws, size_t ws_bytes, janus_stream_t stream) {
+  JANUS_REQUIRE(wt, JANUS_MOE_EINVAL, "janus_moe_block_forward_nvfp4: null weights");
+  const BlockView v = view_of(wt);
+  return block_forward(&v, x, valid, T, out, topk_idx, topk_w, ws, ws_bytes, (hipStream_t)stream, nullptr);
 }
 
 namespace {
@@ -393,7 +438,8 @@ extern "C" int janus_moe_block_forward_noalloc(const janus_moe_block_weights* wt
                 "janus_moe_block_forward_masked with a workspace)", T, need, (size_t)JANUS_MOE_NOALLOC_SCRATCH_BYTES);
   void* ws = scratch_address();
   JANUS_REQUIRE(ws, JANUS_MOE_ELAUNCH, "janus_moe_block_forward_noalloc: hipGetSymbolAddress of the scratch failed");
-  return block_forward(wt, x, valid, T, out, topk_idx, topk_w, ws, JANUS_MOE_NOALLOC_SCRATCH_BYTES,
+  const BlockView v = view_of(wt);
+  return block_forward(&v, x, valid, T, out, topk_idx, topk_w, ws, JANUS_MOE_NOALLOC_SCRATCH_BYTES,
                        (hipStream_t)stream, nullptr);
 }
 
@@ -417,7 +463,8 @@ extern "C" int janus_moe_block_forward_serve(const janus_moe_block_weights* wt, 
   rc = launch_add_rmsnorm(x, h_attn, post_norm_w, post_eps, nullptr, T, wt->H, x_out, h_out, s);
   if (rc) return rc;
   const ServeEpilogue serve = {x_out, next_norm_w, next_eps, next_valid, h_out};
-  return block_forward(wt, h_out, valid, T, nullptr, topk_idx, topk_w, ws, ws_bytes, s, &serve);
+  const BlockView v = view_of(wt);
+  return block_forward(&v, h_out, valid, T, nullptr, topk_idx, topk_w, ws, ws_bytes, s, &serve);
 }
 
 extern "C" int janus_moe_dequant(const int32_t* q, const uint16_t* s, long rows, int K, uint16_t* out,

@@ -34,13 +34,14 @@ struct GemmParams {
   const int* sorted_ids;      // assignment id at each permuted position (< A on real rows)
   int topk, A, T;
   int codec;                  // 0: int4 group-128 (q words, s bf16 [E, N, K/128]); 1: NVFP4 (q bytes, s e4m3
-                              // [E, N, K/16], gsc fp32 [E, N]); the shared expert is int4 only
+                              // [E, N, K/16], gsc fp32 [E, N]); the shared expert uses the same codec
   const int32_t* q;           // routed weight words [E, N, K/8] (NVFP4: the same bytes, [E, N, K/2] uint8)
   const uint16_t* s;          // routed scales (bytes of the codec's scale layout)
   const float* gsc;           // NVFP4: global scale per routed weight row [E, N]
   int N, K;                   // routed weight rows and reduction length
-  const int32_t* q_sh;        // shared expert [N_sh, K_sh/8], null = none
-  const uint16_t* s_sh;
+  const int32_t* q_sh;        // shared expert [N_sh, K_sh/8] (NVFP4: bytes [N_sh, K_sh/2]), null = none
+  const uint16_t* s_sh;       // its scales in the codec's layout
+  const float* gsc_sh;        // NVFP4: global scale per shared weight row [N_sh]
   int N_sh, K_sh;
   const int4* chunks;         // (expert, first position, rows, 0)
   const int* num_chunks;      // device count of valid chunks

@@ -58,10 +58,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 //   issue_a(slot, kb) / issue_b(slot, kb)   stage kb's activation tile into LDS slot / weights into register slot
 //   wait_b(slot, kb)                        the empty asm on stage kb's weight registers (ring slot `slot`)
 //   compute(slot, kb)                       MFMAs of stage kb, held in slot `slot`
-template <int NKB, typename IssueA, typename IssueB, typename WaitB, typename Compute>
+//   before(kb)                              the caller's own loads for after the k loop, issued ahead of stage kb's
+//                                           MFMAs (so their latency hides behind the last stages)
+template <int NKB, typename IssueA, typename IssueB, typename WaitB, typename Compute, typename Before>
 __device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool active, IssueA&& issue_a,
                                                                    IssueB&& issue_b, WaitB&& wait_b,
-                                                                   Compute&& compute) {
+                                                                   Compute&& compute, Before&& before) {
   constexpr int ahead = kStages - 1;
   auto step = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
@@ -72,6 +74,7 @@ __device__ __attribute__((always_inline)) inline void run_pipeline(int nkb, bool
       asm volatile("" ::: "memory");  // the compiler may not hoist the weight loads above the activation loads
       issue_b(Slot<(slot + ahead) % kStages>{}, kb + ahead);
     }
+    before(kb);
     if (active) compute(slot_c, kb);
   };
   static_for<ahead>([&](auto s_c) __attribute__((always_inline)) {
@@ -211,12 +214,16 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     rows = min(kChunkRows, p.T - pos0);
     wq = p.q_sh;
     wsc = reinterpret_cast<const unsigned char*>(p.s_sh);
+    if (CODEC == kNvfp4) wgl = p.gsc_sh;
     N = p.N_sh;
     K = p.K_sh;
   } else {
+    // the count and the entry are loaded together (one memory round trip): r < max_chunks is inside the list, and an
+    // entry past the count is not used
     const int r = c - p.n_shared_chunks;
-    if (r >= *p.num_chunks) return;
+    const int nch = *p.num_chunks;
     const int4 ch = p.chunks[r];
+    if (r >= nch) return;
     pos0 = ch.y;
     rows = ch.z;
     N = p.N;
@@ -378,8 +385,29 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       }
     }
   };
+  // down: each row's assignment id (the token, for the shared expert) and its routing weight, for the epilogue. The
+  // ids are loaded ahead of the second-to-last stage and the weights, which need them, ahead of the last, so neither
+  // waits after the k loop. (Rows past the chunk read its first row's: loads without a branch, values not used.)
+  int id[kRowBlocks];
+  float wt[kRowBlocks];
+  auto before = [&](int kb) __attribute__((always_inline)) {
+    if constexpr (MODE == kDown) {
+      if (kb == (nkb >= 2 ? nkb - 2 : 0)) {
+#pragma unroll
+        for (int rb = 0; rb < kRowBlocks; ++rb) {
+          const int m = rb * 16 + nl;
+          id[rb] = shared ? pos0 + (m < rows ? m : 0) : p.sorted_ids[pos0 + (m < rows ? m : 0)];
+        }
+      }
+      if (kb == nkb - 1) {
+#pragma unroll
+        for (int rb = 0; rb < kRowBlocks; ++rb)
+          wt[rb] = shared ? (p.gamma ? p.gamma[id[rb]] : 1.0f) : p.route_w[id[rb]];
+      }
+    }
+  };
   static_assert(kColBlocks == 4, "wait_b lists every column block");
-  run_pipeline<NKB>(nkb, active, issue_a, load_b, wait_b, compute);
+  run_pipeline<NKB>(nkb, active, issue_a, load_b, wait_b, compute, before);
   if (!active) return;
 
   // ---- epilogue: lane holds rows 16 rb + nl, columns 16 cb + 4 g + i ----
@@ -408,35 +436,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       }
     }
   } else {
-    // every row's assignment id, then its routing weight, before the first store: as far as the compiler knows the
-    // slots may alias the routing weights, and a load written after a row block's stores would wait for them, one
-    // memory round trip per row block
-    // (rows past the chunk read its first row's: loads without a branch, whose values are not used)
-    int id[kRowBlocks];
-    float wt[kRowBlocks];
-    if (shared) {
-#pragma unroll
-      for (int rb = 0; rb < kRowBlocks; ++rb) {
-        const int m = rb * 16 + nl;
-        id[rb] = pos0 + (m < rows ? m : 0);  // the token
-      }
-      if (p.gamma) {
-#pragma unroll
-        for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = p.gamma[id[rb]];
-      } else {
-#pragma unroll
-        for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = 1.0f;
-      }
-    } else {
-#pragma unroll
-      for (int rb = 0; rb < kRowBlocks; ++rb) {
-        const int m = rb * 16 + nl;
-        id[rb] = p.sorted_ids[pos0 + (m < rows ? m : 0)];
-      }
-#pragma unroll
-      for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = p.route_w[id[rb]];
-    }
-    // each row's slot offset, also before the first store (a divisor constant the compiler keeps in scratch would
+    // each row's slot offset, before the first store (a divisor constant the compiler keeps in scratch would
     // otherwise be reloaded, and waited for, between the stores)
     long orow_off[kRowBlocks];
 #pragma unroll
@@ -686,8 +686,9 @@ int launch_gemm(const GemmParams& params, hipStream_t stream) {
   const long grid = (long)ceil_div(total, 8) * 8 * p.nslab;
   JANUS_REQUIRE(grid < (1l << 31), JANUS_MOE_EINVAL, "grouped GEMM grid too large");
   const dim3 g((unsigned)grid), b(kThreads);
-  JANUS_REQUIRE(p.codec == kInt4 || (p.codec == kNvfp4 && p.gsc && p.n_shared_chunks == 0), JANUS_MOE_EINVAL,
-                "grouped GEMM: codec %d (NVFP4 needs global scales and no shared chunks)", p.codec);
+  JANUS_REQUIRE(p.codec == kInt4 || (p.codec == kNvfp4 && p.gsc && (p.n_shared_chunks == 0 || p.gsc_sh)),
+                JANUS_MOE_EINVAL, "grouped GEMM: codec %d (NVFP4 needs global scales, the shared expert's too)",
+                p.codec);
 #define JANUS_GEMM_CASES(CODEC)                                                                          \
   switch (nkb) {                                                                                        \
     case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2, CODEC>), g, b, 0, stream, p); break;         \
@@ -751,7 +752,8 @@ int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* 
     hipLaunchKernelGGL((moe_experts_kernel<16, 4, kInt4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
   else if (gu.codec == kInt4 && nkb_gu == 4 && nkb_dn == 2)
     hipLaunchKernelGGL((moe_experts_kernel<4, 2, kInt4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
-  else if (gu.codec == kNvfp4 && gu.gsc && dn.gsc && nkb_gu == 16 && nkb_dn == 4)
+  else if (gu.codec == kNvfp4 && gu.gsc && dn.gsc && (gu.n_shared_chunks == 0 || (gu.gsc_sh && dn.gsc_sh)) &&
+           nkb_gu == 16 && nkb_dn == 4)
     hipLaunchKernelGGL((moe_experts_kernel<16, 4, kNvfp4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
   else
     return kNotFused;

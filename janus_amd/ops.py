@@ -374,6 +374,76 @@ def _(x, router_w, router_prep, router_bias, gate_up_q, gate_up_s, down_q, down_
     return (torch.empty_like(x), x.new_empty(T, top_k, dtype=torch.int32), x.new_empty(T, top_k, dtype=torch.float32))
 
 
+@torch.library.custom_op("janus_moe::block_forward_nvfp4", mutates_args=())
+def block_forward_nvfp4(x: Tensor, router_w: Tensor, router_prep: Tensor, router_bias: Optional[Tensor],
+                        gate_up: Tensor, gate_up_scale: Tensor, gate_up_global: Tensor, down: Tensor,
+                        down_scale: Tensor, down_global: Tensor, sh_gate_up: Optional[Tensor],
+                        sh_gate_up_scale: Optional[Tensor], sh_gate_up_global: Optional[Tensor],
+                        sh_down: Optional[Tensor], sh_down_scale: Optional[Tensor], sh_down_global: Optional[Tensor],
+                        sh_gate_w: Optional[Tensor], top_k: int,
+                        valid: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
+    """block_forward with NVFP4 weights: stacks gate_up [E, 2I, H/2] uint8, gate_up_scale [E, 2I, H/16] e4m3 (or
+    uint8 bytes), gate_up_global [E, 2I] fp32 (a [E, 2I, 1] view is accepted), down [E, H, I/2], down_scale
+    [E, H, I/16], down_global [E, H]; the shared expert's gate and up rows stacked the same way, [2 I_s, H/2],
+    [2 I_s, H/16], [2 I_s], and its down [H, I_s/2], [H, I_s/16], [H]."""
+    dev = _require_gpu(x, router_w, router_prep, router_bias, gate_up, gate_up_scale, gate_up_global, down, down_scale,
+                       down_global, sh_gate_up, sh_gate_up_scale, sh_gate_up_global, sh_down, sh_down_scale,
+                       sh_down_global, sh_gate_w)
+    T, H = x.shape
+    E, N2, Hh = gate_up.shape
+    I = N2 // 2
+    if Hh * 2 != H or down.shape != (E, H, I // 2):
+        raise ValueError(f"NVFP4 stacks {tuple(gate_up.shape)} / {tuple(down.shape)} do not match x [{T}, {H}]")
+    as_bytes = lambda t: t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t
+    gate_up_scale, down_scale = as_bytes(gate_up_scale), as_bytes(down_scale)
+    gate_up_global = gate_up_global.reshape(E, 2 * I)
+    down_global = down_global.reshape(E, H)
+    _expect(x, "x", torch.bfloat16, (T, H))
+    _expect(router_w, "router_w", torch.float32, (E, H))
+    _expect(gate_up, "gate_up", torch.uint8, (E, 2 * I, H // 2))
+    _expect(gate_up_scale, "gate_up_scale", torch.uint8, (E, 2 * I, H // 16))
+    _expect(gate_up_global, "gate_up_global", torch.float32, (E, 2 * I))
+    _expect(down, "down", torch.uint8, (E, H, I // 2))
+    _expect(down_scale, "down_scale", torch.uint8, (E, H, I // 16))
+    _expect(down_global, "down_global", torch.float32, (E, H))
+    if router_bias is not None:
+        _expect(router_bias, "router_bias", torch.float32, (E,))
+    I_s = 0
+    if sh_gate_up is not None:
+        I_s = sh_gate_up.shape[0] // 2
+        sh_gate_up_scale, sh_down_scale = as_bytes(sh_gate_up_scale), as_bytes(sh_down_scale)
+        sh_gate_up_global, sh_down_global = sh_gate_up_global.reshape(2 * I_s), sh_down_global.reshape(H)
+        _expect(sh_gate_up, "sh_gate_up", torch.uint8, (2 * I_s, H // 2))
+        _expect(sh_gate_up_scale, "sh_gate_up_scale", torch.uint8, (2 * I_s, H // 16))
+        _expect(sh_gate_up_global, "sh_gate_up_global", torch.float32, (2 * I_s,))
+        _expect(sh_down, "sh_down", torch.uint8, (H, I_s // 2))
+        _expect(sh_down_scale, "sh_down_scale", torch.uint8, (H, I_s // 16))
+        _expect(sh_down_global, "sh_down_global", torch.float32, (H,))
+        if sh_gate_w is not None:
+            _expect(sh_gate_w, "sh_gate_w", torch.bfloat16, (H,))
+    _check_mask(valid, "valid", T, dev)
+    weights = _lib.BlockWeightsNvfp4(H, I, E, top_k, I_s, *[_ptr(t) for t in (
+        router_w, router_prep, router_bias, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global,
+        sh_gate_up, sh_gate_up_scale, sh_gate_up_global, sh_down, sh_down_scale, sh_down_global, sh_gate_w)])
+    ws = _workspace(_lib.lib().janus_moe_block_workspace_bytes(T, H, I, E, top_k, I_s), dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    rw = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().janus_moe_block_forward_nvfp4(ctypes.byref(weights), _ptr(x), _ptr(valid), T, _ptr(out),
+                                                       _ptr(idx), _ptr(rw), _ptr(ws), ws.numel(), _stream(dev)),
+              "janus_moe_block_forward_nvfp4")
+    return out, idx, rw
+
+
+@block_forward_nvfp4.register_fake
+def _(x, router_w, router_prep, router_bias, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global,
+      sh_gate_up, sh_gate_up_scale, sh_gate_up_global, sh_down, sh_down_scale, sh_down_global, sh_gate_w, top_k,
+      valid=None):
+    T = x.shape[0]
+    return (torch.empty_like(x), x.new_empty(T, top_k, dtype=torch.int32), x.new_empty(T, top_k, dtype=torch.float32))
+
+
 @torch.library.custom_op("janus_moe::block_forward_serve", mutates_args=())
 def block_forward_serve(x: Tensor, h_attn: Optional[Tensor], post_norm_w: Tensor, post_eps: float,
                         next_norm_w: Tensor, next_eps: float, router_w: Tensor, router_prep: Tensor,

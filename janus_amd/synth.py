@@ -139,3 +139,38 @@ def layer(cfg: LayerConfig, seed: int = 17) -> dict[str, torch.Tensor | None]:
             "sh_gate_w": bf16_tensor(bf16_bits(normals(seed, "sh_gate_w", H) * 0.02), (H,)),
         })
     return w
+
+
+def nvfp4_layer(cfg: LayerConfig, seed: int = 17, device="cpu") -> dict[str, torch.Tensor | None]:
+    """The layer of `layer(cfg, seed)` in the checkpoint's NVFP4 format: its int4 weights decoded and quantised again
+    with ModelOpt's recipe, one global scale per expert projection (gate, up, down) as a load_nvfp4 checkpoint holds
+    them. Keys: router_w, router_bias, sh_gate_w as in `layer`; gate_up [E, 2I, H/2] uint8, gate_up_scale
+    [E, 2I, H/16] float8_e4m3fn, gate_up_global [E, 2I] fp32 (each row's projection global), down / down_scale /
+    down_global [E, H, I/2], [E, H, I/16], [E, H]; with a shared expert sh_gate_up ([2 I_s, H/2], [2 I_s, H/16],
+    [2 I_s]) and sh_down ([H, I_s/2], [H, I_s/16], [H]) likewise. Tensors on `device` (the quantisation runs there)."""
+    from .hybrid import int4_dequantize, nvfp4_quantize
+
+    w = layer(cfg, seed)
+    I, I_s = cfg.I, cfg.I_s
+
+    def encode(parts):  # float projections [rows, K] -> stacked packed, scales, per-row globals
+        enc = [nvfp4_quantize(t) for t in parts]
+        return (torch.cat([e[0] for e in enc]), torch.cat([e[1] for e in enc]),
+                torch.cat([e[2].reshape(1).expand(t.shape[0]) for e, t in zip(enc, parts)]).float())
+
+    def stacks(q, s, split):
+        out = [encode([*(f[:split], f[split:])] if split else [f])
+               for f in int4_dequantize(q.to(device), s.to(device), torch.float32)]
+        return [torch.stack([o[i] for o in out]) for i in range(3)]
+
+    out = {"router_w": w["router_w"].to(device), "sh_gate_w": None if w.get("sh_gate_w") is None else
+           w["sh_gate_w"].to(device),
+           "router_bias": None if w["router_bias"] is None else w["router_bias"].to(device)}
+    out["gate_up"], out["gate_up_scale"], out["gate_up_global"] = stacks(w["gate_up_q"], w["gate_up_s"], I)
+    out["down"], out["down_scale"], out["down_global"] = stacks(w["down_q"], w["down_s"], 0)
+    if I_s:
+        f = int4_dequantize(w["sh_gate_up_q"].to(device), w["sh_gate_up_s"].to(device), torch.float32)
+        out["sh_gate_up"], out["sh_gate_up_scale"], out["sh_gate_up_global"] = encode([f[:I_s], f[I_s:]])
+        f = int4_dequantize(w["sh_down_q"].to(device), w["sh_down_s"].to(device), torch.float32)
+        out["sh_down"], out["sh_down_scale"], out["sh_down_global"] = encode([f])
+    return out

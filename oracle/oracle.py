@@ -253,11 +253,14 @@ def expert_sum_nvfp4(x, idx, weights, gate_up, gate_up_scale, gate_up_global, do
 
 def shared_sum(x, gate_up_q, gate_up_s, down_q, down_s, gate_w=None, tokens=None) -> np.ndarray:
     """Unrounded sigmoid(x . gate_w) * down(RNE_bf16(silu(gate(x)) * up(x))) (fp64) -> [n, H]."""
+    return shared_sum_dq(x, dequant(gate_up_q, gate_up_s), dequant(down_q, down_s), gate_w, tokens)
+
+
+def shared_sum_dq(x, wgu, wd, gate_w=None, tokens=None) -> np.ndarray:
+    """shared_sum with the dequantised weights wgu [2 I_s, H] (gate rows first) and wd [H, I_s]."""
     x = np.asarray(x, dtype=np.float64)
     xs = x if tokens is None else x[np.asarray(tokens)]
-    I_s = np.asarray(gate_up_q).shape[0] // 2
-    wgu = dequant(gate_up_q, gate_up_s)
-    wd = dequant(down_q, down_s)
+    I_s = np.asarray(wgu).shape[0] // 2
     h = bf16_round(silu(xs @ wgu[:I_s].T) * (xs @ wgu[I_s:].T))
     y = h @ wd.T
     if gate_w is not None:
@@ -278,9 +281,26 @@ def block_forward(layer: dict, x, k: int, tokens=None):
     return bf16_round(acc), idx, weights, l
 
 
+def block_forward_nvfp4(layer: dict, x, k: int, tokens=None):
+    """block_forward on NVFP4 weights (the layer load_nvfp4 builds, janus/hybrid.py:1462-1475): `layer` holds
+    router_w (, router_bias), the routed stacks gate_up / gate_up_scale / gate_up_global / down / down_scale /
+    down_global ([E, N, K/2] uint8, [E, N, K/16] e4m3 bytes, [E, N] fp32) and optionally the shared expert's
+    sh_gate_up ... sh_down_global ([2 I_s, H/2], [2 I_s, H/16], [2 I_s]; [H, I_s/2], [H, I_s/16], [H]) and sh_gate_w."""
+    x = np.asarray(x, dtype=np.float64)
+    xs = x if tokens is None else x[np.asarray(tokens)]
+    idx, weights, l = route(xs, layer["router_w"], k, layer.get("router_bias"))
+    acc = expert_sum_nvfp4(xs, idx, weights, layer["gate_up"], layer["gate_up_scale"], layer["gate_up_global"],
+                           layer["down"], layer["down_scale"], layer["down_global"])
+    if layer.get("sh_gate_up") is not None:
+        acc = acc + shared_sum_dq(
+            xs, nvfp4_dequant(layer["sh_gate_up"], layer["sh_gate_up_scale"], layer["sh_gate_up_global"]),
+            nvfp4_dequant(layer["sh_down"], layer["sh_down_scale"], layer["sh_down_global"]), layer.get("sh_gate_w"))
+    return bf16_round(acc), idx, weights, l
+
+
 def numpy_layer(layer: dict) -> dict:
-    """A synth.layer dict of torch tensors -> numpy arrays the oracle reads (bf16 as uint16 bits, router as fp32,
-    the shared gate as bf16 values in fp64)."""
+    """A synth.layer (or synth.nvfp4_layer) dict of torch tensors -> numpy arrays the oracle reads (bf16 as uint16
+    bits, e4m3 as its bytes, router as fp32, the shared gate as bf16 values in fp64)."""
     import torch
 
     out = {}
@@ -290,6 +310,8 @@ def numpy_layer(layer: dict) -> dict:
         elif t.dtype == torch.bfloat16:
             bits = t.contiguous().view(torch.int16).numpy().view(np.uint16)
             out[name] = bf16_from_bits(bits) if name == "sh_gate_w" else bits
+        elif t.dtype == torch.float8_e4m3fn:
+            out[name] = t.contiguous().view(torch.uint8).numpy()
         else:
             out[name] = t.numpy()
     return out

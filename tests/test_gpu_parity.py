@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from janus_amd import ops, synth
-from janus_amd.block import W4A16SparseMoeBlock
+from janus_amd.block import NVFP4SparseMoeBlock, W4A16SparseMoeBlock
 from janus_amd.moe_w4a16 import align, fused_moe
 from oracle import oracle as O
 
@@ -608,3 +608,46 @@ def test_block_serve_equals_the_unfused_chain(gpu, name, rows):
     assert_layer_close(bf16_np(xo)[keep], bf16_np(rx2)[keep], f"{name} residual")
     assert_layer_close(bf16_np(ho)[keep], bf16_np(rh)[keep], f"{name} next norm")
     assert not bf16_np(ho)[~keep].any()
+
+
+# ---- NVFP4 whole block -----------------------------------------------------------------------------------------
+
+NVFP4_SMALL = synth.LayerConfig("nvfp4_small", T=100, H=512, E=32, k=4, I=256, I_s=256)
+
+
+def _nvfp4_block_call(blk, x, valid=None):
+    ex = blk.experts
+    return ops.block_forward_nvfp4(
+        x, blk.gate.weight, blk.gate.prep(), blk.gate.bias, ex.gate_up, ex.gate_up_scale, ex.gate_up_global, ex.down,
+        ex.down_scale, ex.down_global, blk.sh_gate_up, blk.sh_gate_up_scale, blk.sh_gate_up_global, blk.sh_down,
+        blk.sh_down_scale, blk.sh_down_global, blk._shared_gate_w(), blk.gate.top_k, valid)
+
+
+@pytest.mark.parametrize("name", ["nvfp4_small", "short"])
+def test_nvfp4_block_matches_oracle(gpu, name, monkeypatch):
+    """The layer with the checkpoint's NVFP4 weights, routed and shared experts both decoded inside the HIP GEMMs
+    (at the 35B-A3B shape through the persistent launch, shared chunks included), against the oracle's NVFP4 block:
+    routing bit-exact, output to the layer bar; the module's forward is the same call; one launch per GEMM gives the
+    same bits; a right-padding mask leaves the real rows bit-identical and zeroes the padding rows."""
+    cfg = NVFP4_SMALL if name == "nvfp4_small" else synth.CONFIGS[name]
+    L = synth.nvfp4_layer(cfg, device=gpu)
+    blk = NVFP4SparseMoeBlock.from_tensors(L, cfg.k)
+    x = synth.activations(cfg).to(gpu)
+    with torch.no_grad():
+        out, idx, w = _nvfp4_block_call(blk, x)
+        module_out = blk(x)
+        monkeypatch.setenv("JANUS_MOE_SCHEDULE", "split")
+        split, _, _ = _nvfp4_block_call(blk, x)
+        monkeypatch.delenv("JANUS_MOE_SCHEDULE")
+        valid = torch.ones(cfg.T, dtype=torch.bool, device=gpu)
+        valid[cfg.T * 3 // 4:] = False
+        masked, _, _ = _nvfp4_block_call(blk, x, valid)
+    torch.cuda.synchronize()
+    ref, ridx, rw, _ = O.block_forward_nvfp4(O.numpy_layer({k: None if v is None else v.cpu() for k, v in L.items()}),
+                                             bf16_np(x.cpu()), cfg.k)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-4, atol=1e-6)
+    assert_layer_close(bf16_np(out.cpu()), ref, name)
+    assert torch.equal(module_out, out) and torch.equal(split, out)
+    assert torch.equal(masked[valid], out[valid]) and not masked[~valid].any()
+    ops.check_device_status(gpu)

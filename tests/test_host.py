@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from janus_amd import _lib, hybrid, ops, synth
-from janus_amd.block import W4A16SparseMoeBlock
+from janus_amd.block import NVFP4SparseMoeBlock, W4A16SparseMoeBlock
 from janus_amd.moe_w4a16 import align, fused_moe
 from oracle import oracle as O
 
@@ -196,6 +196,26 @@ def test_cpu_expert_paths_agree_with_oracle(monkeypatch, kernel):
         out = blk.experts(x, torch.from_numpy(idx), torch.from_numpy(w))
     n = O.numpy_layer(Lw)
     ref = O.expert_sum(xv, idx, w, n["gate_up_q"], n["gate_up_s"], n["down_q"], n["down_s"])
+    got = O.bf16_values(out)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
+
+
+NVFP4_SMALL = synth.LayerConfig("nvfp4_small", T=100, H=512, E=32, k=4, I=256, I_s=256)
+
+
+def test_cpu_nvfp4_block_matches_oracle():
+    """The NVFP4 block (NVFP4 routed and shared experts, as load_nvfp4 leaves a layer) through its CPU composition,
+    whose decode is torch's (hybrid.nvfp4_dequantize), against the oracle's NVFP4 block, whose decode is numpy's:
+    the two share no code. The CPU path rounds like the reference (bf16 GEMM outputs), hence the looser bar."""
+    cfg = NVFP4_SMALL
+    Lw = synth.nvfp4_layer(cfg)
+    blk = NVFP4SparseMoeBlock.from_tensors(Lw, cfg.k)
+    x = synth.activations(cfg)
+    with torch.no_grad():
+        out = blk(x)
+    ref, idx, _, _ = O.block_forward_nvfp4(O.numpy_layer(Lw), O.bf16_values(x), cfg.k)
+    _, _, tidx = blk.gate(x)
+    assert (tidx.numpy() == idx).mean() > 0.99
     got = O.bf16_values(out)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
 

@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import json
 
+import numpy as np
 import pytest
 import torch
 
@@ -166,3 +167,35 @@ def test_loaded_moe_block_runs_fused_on_the_gpu(gpu, tmp_path, codec):
         out = block.to(gpu)(x.to(gpu)).float().cpu()
     torch.testing.assert_close(out, ref, atol=2e-2, rtol=2e-2)
     assert (out - ref).abs().max() < 0.02 * ref.abs().max() + 1e-3
+
+
+@pytest.mark.gpu
+def test_loaded_nvfp4_layer_runs_as_one_block_call_on_the_gpu(gpu, tmp_path):
+    """A loaded layer's block with its NVFP4 weights as stored (routed experts and the shared expert's NVFP4Linear
+    projections), wrapped as NVFP4SparseMoeBlock: on the GPU the whole block is one janus_moe::block_forward_nvfp4
+    call; against the HF block on the CPU (the reference's dequantise-per-call paths) with the reference test's bar
+    (tests/test_hybrid.py:725-746), and against the oracle's NVFP4 block to the layer bar."""
+    from janus_amd.block import NVFP4SparseMoeBlock
+    from oracle import oracle as O
+
+    _checkpoint(tmp_path)
+    lm = load_nvfp4(_meta_model(), tmp_path)
+    mlp = lm.layers[0].mlp
+    x = (torch.randn(37, H, generator=torch.Generator().manual_seed(5)) * 0.5).bfloat16()
+    with torch.no_grad():
+        ref = mlp(x[None]).float()[0]
+        blk = NVFP4SparseMoeBlock.from_module(mlp).to(gpu)
+        out = blk(x.to(gpu)).float().cpu()
+    torch.testing.assert_close(out, ref, atol=2e-2, rtol=2e-2)
+    assert (out - ref).abs().max() < 0.02 * ref.abs().max() + 1e-3
+    ex, sh = mlp.experts, blk
+    layer = {"router_w": mlp.gate.weight.detach().float(), "router_bias": None,  # the loaded router is bf16
+             "gate_up": ex.gate_up, "gate_up_scale": ex.gate_up_scale, "gate_up_global": ex.gate_up_global[..., 0],
+             "down": ex.down, "down_scale": ex.down_scale, "down_global": ex.down_global[..., 0],
+             "sh_gate_w": mlp.shared_expert_gate.weight.detach().reshape(-1).bfloat16()}
+    for name in ("sh_gate_up", "sh_gate_up_scale", "sh_gate_up_global", "sh_down", "sh_down_scale", "sh_down_global"):
+        layer[name] = getattr(sh, name).cpu()
+    want = O.block_forward_nvfp4(O.numpy_layer({k: None if v is None else v.cpu() for k, v in layer.items()}),
+                                 O.bf16_values(x), 2)[0]
+    got = O.bf16_values(out.bfloat16())
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-3
