@@ -131,6 +131,23 @@ JANUS_MOE_API int janus_moe_experts_nvfp4(const uint16_t* x, const int64_t* top_
                                           uint16_t* out, void* ws, size_t ws_bytes, janus_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------
+ * fused_moe with a reused tile plan (janus/moe_w4a16.py:122-140, `plan=`; the plan comes from align() at :129-130):
+ * plan_sorted_ids [tiles * block] and plan_expert_ids [tiles] int64, tiles = ceil((S*top_k + E*(block-1)) / block),
+ * as janus_moe_align(top_k_index, E, block) writes them for this top_k_index. The align launch is skipped; the
+ * GEMMs take their row order from the plan (the same rows in the same order per expert, so the output is bit for bit
+ * that of janus_moe_experts / janus_moe_experts_nvfp4). codec 0: int4 (gate_up = int32 words, scales bf16, globals
+ * NULL), 1: NVFP4 (as janus_moe_experts_nvfp4). A plan for another top_k_index gives a wrong result, but every
+ * access stays in bounds. */
+JANUS_MOE_API size_t janus_moe_experts_planned_workspace_bytes(int S, int top_k, int E, int H, int I, int block);
+JANUS_MOE_API int janus_moe_experts_planned(int codec, const uint16_t* x, const int64_t* top_k_index,
+                                            const float* top_k_weights, const void* gate_up, const void* gate_up_scale,
+                                            const float* gate_up_global, const void* down, const void* down_scale,
+                                            const float* down_global, const int64_t* plan_sorted_ids,
+                                            const int64_t* plan_expert_ids, int block, int S, int H, int I, int E,
+                                            int top_k, uint16_t* out, void* ws, size_t ws_bytes,
+                                            janus_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------
  * Replaces nvfp4_dequantize (janus/hybrid.py:426-437) and with it NVFP4Experts.gate_up_proj / down_proj
  * (:539-545): out [rows, K] bf16 from packed [rows, K/2] uint8, scale [rows, K/16] e4m3 bytes, global [rows] fp32,
  * by the device decode the GEMMs use. K % 16 == 0; stacks [E, N, K] are rows = E * N. */

@@ -24,6 +24,7 @@ EXPORTS = (
     "janus_moe_dequant", "janus_moe_profile_events",
     "janus_moe_experts_nvfp4", "janus_moe_dequant_nvfp4", "janus_moe_device_status",
     "janus_moe_block_forward_noalloc", "janus_moe_block_forward_nvfp4",
+    "janus_moe_experts_planned_workspace_bytes", "janus_moe_experts_planned",
 )
 
 _p, _i, _z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -77,6 +78,8 @@ _SIGNATURES = {
     "janus_moe_device_status": (_i, [_p, _i, _p]),
     "janus_moe_block_forward_noalloc": (_i, [ctypes.POINTER(BlockWeights), _p, _p, _i, _p, _p, _p, _p]),
     "janus_moe_block_forward_nvfp4": (_i, [ctypes.POINTER(BlockWeightsNvfp4), _p, _p, _i, _p, _p, _p, _p, _z, _p]),
+    "janus_moe_experts_planned_workspace_bytes": (_z, [_i] * 6),
+    "janus_moe_experts_planned": (_i, [_i] + [_p] * 11 + [_i] * 6 + [_p, _p, _z, _p]),
 }
 
 _handle = None

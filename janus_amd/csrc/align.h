@@ -26,4 +26,11 @@ int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace&
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks, int* clear,
                  int clear_n, int* status, hipStream_t stream);
 
+// The GEMM chunk list and int32 permutation from a caller's reference tile plan (sorted_ids [tiles * block],
+// expert_ids [tiles], int64, as align() returns them for some block), in place of an align launch; clear[0 .. clear_n)
+// is zeroed as align does.
+int launch_plan_chunks(const int64_t* plan_sorted_ids, const int64_t* plan_expert_ids, int tiles, int block, int A,
+                       int E, int* sorted_ids, int4* chunks, int capacity, int chunk_rows, int* num_chunks, int* clear,
+                       int clear_n, hipStream_t stream);
+
 }  // namespace janus

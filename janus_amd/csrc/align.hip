@@ -438,6 +438,69 @@ AlignWorkspace carve_align(Carver& c, int A, int E) {
   return w;
 }
 
+namespace {
+// First index in [lo, hi) whose value is >= key, for values non-decreasing over [lo, hi).
+__device__ int lower_bound64(const int64_t* __restrict__ v, int lo, int hi, int64_t key) {
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (v[mid] < key) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// The GEMM chunk list from a caller's reference tile plan (align() at any block size): thread e finds expert e's
+// tiles by binary search over expert_ids (non-decreasing; tiles past the total hold ids >= E) and its real rows by
+// binary search for the first sentinel in them (real assignment ids come first), then cuts those rows into chunks.
+// The permutation is copied as is (values outside [0, A] become the sentinel A), and clear[0 .. clear_n) is zeroed.
+// A plan that does not come from align cannot make the GEMMs go out of bounds: chunks stay inside the plan's rows
+// and the list's capacity, and the GEMMs skip rows whose id is not below A.
+__global__ void __launch_bounds__(kScanThreads) plan_chunks_kernel(
+    const int64_t* __restrict__ psorted, const int64_t* __restrict__ pexpert, int tiles, int block, int A, int E,
+    int* __restrict__ sorted_ids, int4* __restrict__ chunks, int capacity, int chunk_rows, int* __restrict__ num_chunks,
+    int* __restrict__ clear, int clear_n) {
+  __shared__ int waves[16];
+  const int tid = threadIdx.x;
+  const int P = tiles * block;
+  for (int i = tid; i < P; i += blockDim.x) {
+    const int64_t v = psorted[i];
+    sorted_ids[i] = (v >= 0 && v < A) ? (int)v : A;
+  }
+  for (int i = tid; i < clear_n; i += blockDim.x) clear[i] = 0;
+  int start = 0, count = 0;
+  if (tid < E) {
+    const int lo = lower_bound64(pexpert, 0, tiles, tid), hi = lower_bound64(pexpert, lo, tiles, tid + 1);
+    start = lo * block;
+    // rows [start, start + count): the ids below A before the expert's first sentinel
+    int a = start, b = hi * block;
+    while (a < b) {
+      const int mid = (a + b) >> 1;
+      const int64_t v = psorted[mid];
+      if (v >= 0 && v < A) a = mid + 1;
+      else b = mid;
+    }
+    count = a - start;
+  }
+  const int nch = (count + chunk_rows - 1) / chunk_rows;
+  const int end = block_inclusive_scan(nch, waves);
+  for (int j = 0; j < nch; ++j) {
+    const int at = end - nch + j;
+    if (at < capacity) chunks[at] = make_int4(tid, start + j * chunk_rows, min(chunk_rows, count - j * chunk_rows), 0);
+  }
+  if (tid == (int)blockDim.x - 1) *num_chunks = min(end, capacity);
+}
+}  // namespace
+
+int launch_plan_chunks(const int64_t* psorted, const int64_t* pexpert, int tiles, int block, int A, int E,
+                       int* sorted_ids, int4* chunks, int capacity, int chunk_rows, int* num_chunks, int* clear,
+                       int clear_n, hipStream_t stream) {
+  JANUS_REQUIRE(E > 0 && E <= kScanThreads, JANUS_MOE_EINVAL, "plan chunks: E=%d (at most %d)", E, kScanThreads);
+  hipLaunchKernelGGL(plan_chunks_kernel, dim3(1), dim3(kScanThreads), 0, stream, psorted, pexpert, tiles, block, A, E,
+                     sorted_ids, chunks, capacity, chunk_rows, num_chunks, clear, clear_n);
+  JANUS_LAUNCH_CHECK("plan_chunks");
+  return JANUS_MOE_OK;
+}
+
 template <typename IdxT, typename OutT>
 int launch_align(const IdxT* idx, int A, int E, int block, const AlignWorkspace& w, OutT* sorted_ids, int sorted_len,
                  OutT* expert_ids, int tiles, OutT* total, int4* chunks, int chunk_rows, int* num_chunks,

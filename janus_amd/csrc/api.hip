@@ -74,10 +74,11 @@ struct ExpertsWorkspace {
   int P, C, nslots, nsched;
 };
 
-ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I, int I_s) {
+// plan_block > 0: the permuted rows follow a caller's tile plan padded to that block (align() at that block size).
+ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I, int I_s, int plan_block = 0) {
   ExpertsWorkspace w;
   const int A = T * top_k;
-  w.P = A + E * (kRowPad - 1);
+  w.P = plan_block > 0 ? ceil_div(A + E * (plan_block - 1), plan_block) * plan_block : A + E * (kRowPad - 1);
   w.C = ceil_div(A, kChunkRows) + E;
   w.align = carve_align(c, A, E);
   w.sorted_ids = c.take<int>(w.P);
@@ -127,15 +128,21 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
                 const ExpertsWorkspace& w, hipStream_t stream, int codec = 0, const float* gu_global = nullptr,
                 const float* dn_global = nullptr, const uint8_t* valid = nullptr,
                 const ServeEpilogue* serve = nullptr, const int64_t* check_ids = nullptr,
-                const float* sgu_global = nullptr, const float* sdn_global = nullptr) {
+                const float* sgu_global = nullptr, const float* sdn_global = nullptr,
+                const int64_t* plan_sorted_ids = nullptr, const int64_t* plan_expert_ids = nullptr,
+                int plan_block = 0) {
   const int A = T * top_k;
   int* status = device_status_word();
   JANUS_REQUIRE(status, JANUS_MOE_ELAUNCH, "the device status word of this library could not be resolved");
   mark(1, stream);
   // check_ids: the caller's own top-k ids (the experts entries). An id outside [0, E) is dropped by align, reported in
   // the status word, and its slot skipped by the combine. The block path routes padding tokens to id E on purpose.
-  int rc = launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
-                                   kChunkRows, w.num_chunks, w.sched, w.nsched, check_ids ? status : nullptr, stream);
+  int rc = plan_sorted_ids
+               ? launch_plan_chunks(plan_sorted_ids, plan_expert_ids, w.P / plan_block, plan_block, A, E, w.sorted_ids,
+                                    w.chunks, w.C, kChunkRows, w.num_chunks, w.sched, w.nsched, stream)
+               : launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
+                                         kChunkRows, w.num_chunks, w.sched, w.nsched, check_ids ? status : nullptr,
+                                         stream);
   if (rc) return rc;
   const bool shared = I_s > 0;
   GemmParams p = {};
@@ -300,6 +307,44 @@ extern "C" int janus_moe_experts_nvfp4(const uint16_t* x, const int64_t* top_k_i
                               nullptr, nullptr, nullptr, nullptr, nullptr, S, H, I, 0, E, top_k, out, w,
                               (hipStream_t)stream, /*codec=*/1, gate_up_global, down_global, nullptr, nullptr,
                               top_k_index);
+}
+
+extern "C" size_t janus_moe_experts_planned_workspace_bytes(int S, int top_k, int E, int H, int I, int block) {
+  if (S < 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0 || block <= 0) return 0;
+  Carver c(nullptr);
+  carve_experts(c, S, top_k, E, H, I, 0, block);
+  return align_up(c.used, 256);
+}
+
+extern "C" int janus_moe_experts_planned(int codec, const uint16_t* x, const int64_t* top_k_index,
+                                         const float* top_k_weights, const void* gate_up, const void* gate_up_scale,
+                                         const float* gate_up_global, const void* down, const void* down_scale,
+                                         const float* down_global, const int64_t* plan_sorted_ids,
+                                         const int64_t* plan_expert_ids, int block, int S, int H, int I, int E,
+                                         int top_k, uint16_t* out, void* ws, size_t ws_bytes, janus_stream_t stream) {
+  int rc = check_expert_sizes("janus_moe_experts_planned", S, H, I, E, top_k);
+  if (rc) return rc;
+  JANUS_REQUIRE(codec == 0 || codec == 1, JANUS_MOE_EINVAL, "janus_moe_experts_planned: codec %d (0 int4, 1 NVFP4)",
+                codec);
+  JANUS_REQUIRE(block > 0 && block <= 1024, JANUS_MOE_EINVAL, "janus_moe_experts_planned: block=%d", block);
+  const long tiles = ((long)S * top_k + (long)E * (block - 1) + block - 1) / block;
+  JANUS_REQUIRE(tiles * block * (long)I * 2 < (1l << 31), JANUS_MOE_EINVAL,
+                "janus_moe_experts_planned: the plan's rows (%ld x I=%d bf16) reach 2 GiB", tiles * block, I);
+  if (S == 0) return JANUS_MOE_OK;
+  JANUS_REQUIRE(x && top_k_index && top_k_weights && gate_up && gate_up_scale && down && down_scale && out &&
+                    plan_sorted_ids && plan_expert_ids && (codec == 0 || (gate_up_global && down_global)),
+                JANUS_MOE_EINVAL, "janus_moe_experts_planned: null pointer");
+  const size_t need = janus_moe_experts_planned_workspace_bytes(S, top_k, E, H, I, block);
+  JANUS_REQUIRE(ws && ws_bytes >= need, JANUS_MOE_EWORKSPACE, "janus_moe_experts_planned: workspace %zu < %zu bytes",
+                ws_bytes, need);
+  Carver c(ws);
+  ExpertsWorkspace w = carve_experts(c, S, top_k, E, H, I, 0, block);
+  mark(0, (hipStream_t)stream);
+  return run_experts<int64_t>(x, top_k_index, top_k_weights, static_cast<const int32_t*>(gate_up),
+                              static_cast<const uint16_t*>(gate_up_scale), static_cast<const int32_t*>(down),
+                              static_cast<const uint16_t*>(down_scale), nullptr, nullptr, nullptr, nullptr, nullptr,
+                              S, H, I, 0, E, top_k, out, w, (hipStream_t)stream, codec, gate_up_global, down_global,
+                              nullptr, nullptr, top_k_index, nullptr, nullptr, plan_sorted_ids, plan_expert_ids, block);
 }
 
 extern "C" int janus_moe_dequant_nvfp4(const uint8_t* packed, const uint8_t* scale, const float* global, long rows,

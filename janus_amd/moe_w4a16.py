@@ -33,10 +33,25 @@ def align(top_k_index: torch.Tensor, num_experts: int, block: int):
 def fused_moe(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global,
               plan=None):
     """Routed experts of a MoE block (janus/moe_w4a16.py:122-140): x [S, H], top_k_index [S, k], top_k_weights [S, k]
-    -> [S, H] in x's dtype. `plan`, an `align` result the reference lets callers reuse, is accepted and not needed:
-    the kernels rebuild their own tile plan from top_k_index on the device."""
-    if plan is not None and len(plan) != 3:
-        raise ValueError("plan must be align()'s (sorted_ids, expert_ids, total)")
+    -> [S, H] in x's dtype. `plan`, an `align(top_k_index, E, block)` result for any block, is reused as the
+    reference reuses it: the align launch is skipped and the GEMMs take the plan's row order (the output is the same,
+    bit for bit)."""
+    if plan is not None:
+        if len(plan) != 3:
+            raise ValueError("plan must be align()'s (sorted_ids, expert_ids, total)")
+        sorted_ids, expert_ids, _ = plan
+        dtype = x.dtype
+        E, two_i = gate_up.shape[0], gate_up.shape[1]
+        if gate_up.dtype == torch.uint8 and (gate_up_global is None or down_global is None):
+            raise ValueError("NVFP4 stacks need their global scales")
+        nv = gate_up.dtype == torch.uint8
+        out = ops.experts_planned(
+            x.to(torch.bfloat16).contiguous(), top_k_index.to(torch.int64).contiguous(),
+            top_k_weights.to(torch.float32).contiguous(), gate_up.contiguous(), gate_up_scale.contiguous(),
+            gate_up_global.float().reshape(E, two_i).contiguous() if nv else None, down.contiguous(),
+            down_scale.contiguous(), down_global.float().reshape(E, x.shape[1]).contiguous() if nv else None,
+            sorted_ids.to(torch.int64).contiguous(), expert_ids.to(torch.int64).contiguous())
+        return out.to(dtype)
     if gate_up.dtype == torch.uint8:  # NVFP4
         S, H = x.shape
         E, two_i, h2 = gate_up.shape

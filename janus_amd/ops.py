@@ -300,6 +300,64 @@ def _(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, dow
     return torch.empty_like(x)
 
 
+@torch.library.custom_op("janus_moe::experts_planned", mutates_args=())
+def experts_planned(x: Tensor, top_k_index: Tensor, top_k_weights: Tensor, gate_up: Tensor, gate_up_scale: Tensor,
+                    gate_up_global: Optional[Tensor], down: Tensor, down_scale: Tensor, down_global: Optional[Tensor],
+                    plan_sorted_ids: Tensor, plan_expert_ids: Tensor) -> Tensor:
+    """experts / experts_nvfp4 (by gate_up's dtype: int32 words or uint8 NVFP4) with a reused align() plan
+    (plan_sorted_ids [tiles * block], plan_expert_ids [tiles], int64) in place of the align launch: [S, H] bf16."""
+    dev = _require_gpu(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, down, down_scale,
+                       down_global, plan_sorted_ids, plan_expert_ids)
+    S, H = x.shape
+    k = top_k_index.shape[1]
+    nv = gate_up.dtype == torch.uint8
+    E, two_i, kw = gate_up.shape
+    I = two_i // 2
+    if kw * (2 if nv else 8) != H:
+        raise ValueError(f"gate_up packs K={kw * (2 if nv else 8)}, x has H={H}")
+    tiles = plan_expert_ids.shape[0]
+    block = plan_sorted_ids.shape[0] // max(tiles, 1)
+    if tiles == 0 or block * tiles != plan_sorted_ids.shape[0] or tiles != -(-(S * k + E * (block - 1)) // block):
+        raise ValueError(f"plan: {tuple(plan_sorted_ids.shape)} sorted ids and {tiles} tiles are not align()'s for "
+                         f"S={S}, k={k}, E={E}")
+    _expect(x, "x", torch.bfloat16, (S, H))
+    _expect(top_k_index, "top_k_index", torch.int64, (S, k))
+    _expect(top_k_weights, "top_k_weights", torch.float32, (S, k))
+    _expect(plan_sorted_ids, "plan_sorted_ids", torch.int64, (tiles * block,))
+    _expect(plan_expert_ids, "plan_expert_ids", torch.int64, (tiles,))
+    if nv:
+        gus = gate_up_scale.view(torch.uint8) if gate_up_scale.dtype == torch.float8_e4m3fn else gate_up_scale
+        dns = down_scale.view(torch.uint8) if down_scale.dtype == torch.float8_e4m3fn else down_scale
+        gug, dng = gate_up_global.reshape(E, 2 * I), down_global.reshape(E, H)
+        _expect(gate_up, "gate_up", torch.uint8, (E, 2 * I, H // 2))
+        _expect(gus, "gate_up_scale", torch.uint8, (E, 2 * I, H // 16))
+        _expect(gug, "gate_up_global", torch.float32, (E, 2 * I))
+        _expect(down, "down", torch.uint8, (E, H, I // 2))
+        _expect(dns, "down_scale", torch.uint8, (E, H, I // 16))
+        _expect(dng, "down_global", torch.float32, (E, H))
+    else:
+        gus, dns, gug, dng = gate_up_scale, down_scale, None, None
+        _expect(gate_up, "gate_up_q", torch.int32, (E, 2 * I, H // 8))
+        _expect(gus, "gate_up_s", torch.bfloat16, (E, 2 * I, H // 128))
+        _expect(down, "down_q", torch.int32, (E, H, I // 8))
+        _expect(dns, "down_s", torch.bfloat16, (E, H, I // 128))
+    out = torch.empty(S, H, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    ws = _workspace(L.janus_moe_experts_planned_workspace_bytes(S, k, E, H, I, block), dev)
+    with torch.cuda.device(dev):
+        check(L.janus_moe_experts_planned(int(nv), _ptr(x), _ptr(top_k_index), _ptr(top_k_weights), _ptr(gate_up),
+                                          _ptr(gus), _ptr(gug), _ptr(down), _ptr(dns), _ptr(dng),
+                                          _ptr(plan_sorted_ids), _ptr(plan_expert_ids), block, S, H, I, E, k,
+                                          _ptr(out), _ptr(ws), ws.numel(), _stream(dev)), "janus_moe_experts_planned")
+    return out
+
+
+@experts_planned.register_fake
+def _(x, top_k_index, top_k_weights, gate_up, gate_up_scale, gate_up_global, down, down_scale, down_global,
+      plan_sorted_ids, plan_expert_ids):
+    return torch.empty_like(x)
+
+
 # ---- whole block ---------------------------------------------------------------------------------------------
 
 def _check_mask(mask: Optional[Tensor], name: str, T: int, dev: torch.device):

@@ -651,3 +651,33 @@ def test_nvfp4_block_matches_oracle(gpu, name, monkeypatch):
     assert torch.equal(module_out, out) and torch.equal(split, out)
     assert torch.equal(masked[valid], out[valid]) and not masked[~valid].any()
     ops.check_device_status(gpu)
+
+
+# ---- fused_moe with a reused plan ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("S,E,H,I,k", [(3, 16, 512, 256, 2), (100, 16, 2048, 512, 8), (700, 16, 2048, 512, 8),
+                                       (96, 256, 2048, 512, 8)])
+def test_fused_moe_with_a_reused_plan_equals_its_own_align(gpu, S, E, H, I, k):
+    """fused_moe(plan=align(top_k_index, E, block)) for the reference's block sizes 16, 32 and 64
+    (janus/moe_w4a16.py:129-130): the align launch is skipped and the GEMMs take the plan's row order, and the output
+    equals the call without a plan bit for bit, for both codecs (the 35B-A3B shape runs the persistent launch)."""
+    cfg = synth.LayerConfig("plan", T=S, H=H, E=E, k=k, I=I)
+    L = synth.layer(cfg, 4)
+    g = torch.Generator().manual_seed(S + E)
+    x = (torch.randn(S, H, generator=g) * 0.5).bfloat16().to(gpu)
+    index = torch.randint(0, E, (S, k), generator=g)
+    index[: S // 2, 0] = 3                                             # a hot expert
+    index = index.to(gpu)
+    weights = torch.softmax(torch.randn(S, k, generator=g), -1).to(gpu)
+    i4 = (L["gate_up_q"].to(gpu), L["gate_up_s"].to(gpu), None, L["down_q"].to(gpu), L["down_s"].to(gpu), None)
+    N = synth.nvfp4_layer(cfg, 4, device=gpu)
+    nv = tuple(N[n] for n in ("gate_up", "gate_up_scale", "gate_up_global", "down", "down_scale", "down_global"))
+    with torch.no_grad():
+        for stacks in (i4, nv):
+            want = fused_moe(x, index, weights, *stacks)
+            for block in (16, 32, 64):
+                plan = align(index, E, block)
+                got = fused_moe(x, index, weights, *stacks, plan=plan)
+                torch.cuda.synchronize()
+                assert torch.equal(got, want), block
+    ops.check_device_status(gpu)
