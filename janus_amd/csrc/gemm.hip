@@ -293,7 +293,10 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       n = col0 + 16 * cb + nl;
     if (!active) n = 0;
     woff[cb] = (uint32_t)n * (uint32_t)(K / 2) + g * 16;
-    soff[cb] = (uint32_t)n * (uint32_t)(K / KS * C::kScaleBytesPerStage) + (CODEC == kNvfp4 ? g * 2 : 0);
+    // NVFP4: the lane's two block scales of a stage sit at byte 2g of the stage's 8 (unbatched); batched, the lane
+    // loads the 8 bytes of stage 4m + g of each four-stage batch m (see stage_scale)
+    soff[cb] = (uint32_t)n * (uint32_t)(K / KS * C::kScaleBytesPerStage) +
+               (CODEC == kNvfp4 ? (NKB >= 4 && NKB % 4 == 0 ? g * 8 : g * 2) : 0);
     gq[cb] = CODEC == kNvfp4 ? wgl[n] : 0.0f;
   }
 
@@ -306,9 +309,13 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   const int nkb = NKB > 0 ? NKB : K / KS;
   u32x4 bw[kStages][kColBlocks];
   uint32_t sc[kStages][kColBlocks];
-  // int4 scales with the k loop unrolled: one 8-byte load per column block brings the bf16 scales of four stages (the
-  // row's groups 4m .. 4m + 3 are adjacent), issued with the weights of stage 4m; two batches are live at a time
-  constexpr bool kBatchScales = CODEC == kInt4 && NKB >= 4 && NKB % 4 == 0;
+  // Scales with the k loop unrolled come in batches of four stages, one 8-byte load per column block, issued with the
+  // weights of stage 4m; two batches are live at a time.
+  //   int4: the row's bf16 scales of groups 4m .. 4m + 3 (adjacent).
+  //   NVFP4: the row's 32 e4m3 bytes of the batch are 8 per stage; lane g loads stage 4m + g's 8 bytes, and a lane
+  //   takes its two bytes of stage 4m + s (at byte 2g) from lane (nl, s) with two cross-lane reads: one load per four
+  //   stages instead of a 2-byte load every stage.
+  constexpr bool kBatchScales = NKB >= 4 && NKB % 4 == 0;
   u32x2 scb[2][kColBlocks];
 
   // the LDS destination is wave-uniform (it goes to M0) and the stage's k offset rides in the SGPR offset
@@ -327,28 +334,45 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     for (int cb = 0; cb < kColBlocks; ++cb) {
       bw[slot][cb] = *reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2));
       if constexpr (kBatchScales) {
-        if (kb % 4 == 0) scb[(kb / 4) & 1][cb] = *reinterpret_cast<const u32x2*>(sbase + soff[cb] + kb * 2);
+        if (kb % 4 == 0)
+          scb[(kb / 4) & 1][cb] = *reinterpret_cast<const u32x2*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
       } else {
         sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
       }
     }
   };
-  // stage kb's scale bits of column block cb (the batched form keeps the bf16 bits in either half of a word)
+  // stage kb's scale bits of column block cb: int4, the bf16 bits (the batched form keeps them in either half of a
+  // word); NVFP4, the two e4m3 bytes of the lane's blocks
   auto stage_scale = [&](auto slot_c, int kb, int cb) __attribute__((always_inline)) -> uint32_t {
     constexpr int slot = decltype(slot_c)::value;
-    if constexpr (kBatchScales) {
+    if constexpr (kBatchScales && CODEC == kInt4) {
       const u32x2 v = scb[(kb / 4) & 1][cb];
       const uint32_t word = (kb & 2) ? v[1] : v[0];
       return (kb & 1) ? word >> 16 : word & 0xFFFFu;
+    } else if constexpr (kBatchScales) {
+      const u32x2 v = scb[(kb / 4) & 1][cb];
+      const int src = nl + 16 * (kb & 3);  // the lane that loaded stage kb's 8 bytes
+      const uint32_t lo = __shfl((int)v[0], src), hi = __shfl((int)v[1], src);
+      const uint32_t word = (g & 2) ? hi : lo;
+      return (g & 1) ? word >> 16 : word & 0xFFFFu;
     } else {
       return sc[slot][cb];
+    }
+  };
+  // the scale registers of stage kb as loaded (a batch's registers at each of its stages)
+  auto scale_regs = [&](auto slot_c, int kb, int cb) __attribute__((always_inline)) -> u32x2 {
+    constexpr int slot = decltype(slot_c)::value;
+    if constexpr (kBatchScales) {
+      return scb[(kb / 4) & 1][cb];
+    } else {
+      return u32x2{sc[slot][cb], 0u};
     }
   };
   auto wait_b = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
     const u32x4 w0 = bw[slot][0], w1 = bw[slot][1], w2 = bw[slot][2], w3 = bw[slot][3];
-    const uint32_t s0 = stage_scale(slot_c, kb, 0), s1 = stage_scale(slot_c, kb, 1), s2 = stage_scale(slot_c, kb, 2),
-                   s3 = stage_scale(slot_c, kb, 3);
+    const u32x2 s0 = scale_regs(slot_c, kb, 0), s1 = scale_regs(slot_c, kb, 1), s2 = scale_regs(slot_c, kb, 2),
+                s3 = scale_regs(slot_c, kb, 3);
     asm volatile("" ::"v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(s0), "v"(s1), "v"(s2), "v"(s3));
   };
   auto compute = [&](auto slot_c, int kb) __attribute__((always_inline)) {
