@@ -320,13 +320,24 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
 
   // the LDS destination is wave-uniform (it goes to M0) and the stage's k offset rides in the SGPR offset
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  // The last two row blocks are loaded only when the chunk reaches them (each load is one more instruction through
+  // the CU's address unit, which the GEMM keeps busy); their LDS rows otherwise keep older data, read but never
+  // multiplied. They are issued first in a stage's group, so the waits the compiler derives for the paths that skip
+  // them (fewer loads in flight) cost at most those two early loads on the paths that issue them.
+  constexpr int kAlwaysRb = 4;
+  const int unrb = __builtin_amdgcn_readfirstlane(nrb);
   auto issue_a = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
     unsigned char* dst = lds.slot(slot_c) + (4 * uwave) * kRowBytes;
-#pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r)
+    auto load = [&](int r) __attribute__((always_inline)) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (JANUS_LDS void*)(dst + 16 * r * kRowBytes), 16, aoff[r],
                                                kb * (KS * 2), 0, 0);
+    };
+#pragma unroll
+    for (int r = kAlwaysRb; r < kRowBlocks; ++r)
+      if (r < unrb) load(r);
+#pragma unroll
+    for (int r = 0; r < kAlwaysRb; ++r) load(r);
   };
   auto load_b = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
