@@ -140,8 +140,9 @@ class _Norm(torch.nn.Module):
         self.weight, self.eps = weight, eps
 
 
-def variant_timings(cfg, x, blk, dev) -> dict:
+def variant_timings(cfg, x, blk, dev, rounds: int = 3) -> dict:
     """Device time per call (us) of the paths beside the headline layer, on the same inputs:
+      - layer: the headline layer itself, measured in the same rounds as the others (the reference point);
       - masked_25pct: the layer with a level batch's right padding (8 rows, a quarter of the positions padding);
       - serve_unfused / serve_fused: _add_norm, the layer and the next _add_norm as three calls, and as one call whose
         combine writes the second _add_norm;
@@ -149,27 +150,23 @@ def variant_timings(cfg, x, blk, dev) -> dict:
         the same shape (random weights quantised on the GPU);
       - block_nvfp4: the whole layer (router, routed and shared experts) with the same layer's weights re-encoded in
         NVFP4 (synth.nvfp4_layer, quantised on the GPU), one block_forward_nvfp4 call.
-    Each entry that fails is reported as its error text instead."""
-    from janus_amd import ops
+    The paths are timed in `rounds` interleaved rounds and each reports its median, so a clock or box drift during
+    the measurement moves them together. Each entry that fails is reported as its error text instead."""
+    from janus_amd import ops, synth
+    from janus_amd.block import NVFP4SparseMoeBlock
     from janus_amd.hybrid import nvfp4_quantize
     from janus_amd.moe_w4a16 import fused_moe
 
-    out = {}
+    out, cases = {}, {}
     g = torch.Generator(device=dev).manual_seed(5)
-
-    def run(name, fn):
-        try:
-            with torch.no_grad():
-                out[name] = _time_us(fn)
-        except Exception as exc:  # an extra line of evidence must not take the headline measurement with it
-            out[name] = f"{type(exc).__name__}: {exc}"[:200]
+    cases["layer"] = lambda: blk(x)
 
     rows = 8
     length = cfg.T // rows
     lengths = torch.full((rows,), length, device=dev)
     lengths[::2] = length // 2                       # half the rows half full: a quarter of the positions padding
     valid = (torch.arange(length, device=dev)[None] < lengths[:, None]).reshape(-1)
-    run("masked_25pct", lambda: blk(x, valid=valid))
+    cases["masked_25pct"] = lambda: blk(x, valid=valid)
 
     h_attn = (torch.randn(x.shape, generator=g, device=dev) * 0.5).bfloat16()
     post = _Norm((torch.randn(cfg.H, generator=g, device=dev) * 0.1).bfloat16())
@@ -179,33 +176,42 @@ def variant_timings(cfg, x, blk, dev) -> dict:
         x1, n1 = ops.add_rmsnorm(x, h_attn, post.weight, post.eps)
         return ops.add_rmsnorm(x1, blk(n1), nxt.weight, nxt.eps)
 
-    run("serve_unfused", unfused)
-    run("serve_fused", lambda: blk.serve(x, h_attn, post, nxt))
+    cases["serve_unfused"] = unfused
+    cases["serve_fused"] = lambda: blk.serve(x, h_attn, post, nxt)
 
     with torch.no_grad():
         _, w, idx = blk.gate(x)
     ex = blk.experts
-    run("experts_int4", lambda: fused_moe(x, idx, w, ex.gate_up, ex.gate_up_scale, None, ex.down, ex.down_scale, None))
+    cases["experts_int4"] = lambda: fused_moe(x, idx, w, ex.gate_up, ex.gate_up_scale, None, ex.down, ex.down_scale,
+                                              None)
     try:
         def stack(rows_, k):
             parts = [nvfp4_quantize(torch.randn(rows_, k, generator=g, device=dev) * 0.05) for _ in range(cfg.E)]
             return (torch.stack([p[0] for p in parts]), torch.stack([p[1] for p in parts]),
                     torch.stack([p[2] for p in parts])[:, None, None].expand(cfg.E, rows_, 1).contiguous())
-        gu, gus, gug = stack(2 * cfg.I, cfg.H)
-        dn, dns, dng = stack(cfg.H, cfg.I)
-        run("experts_nvfp4", lambda: fused_moe(x, idx, w, gu, gus, gug, dn, dns, dng))
-        del gu, gus, gug, dn, dns, dng
+        nv_stacks = (*stack(2 * cfg.I, cfg.H), *stack(cfg.H, cfg.I))
+        cases["experts_nvfp4"] = lambda: fused_moe(x, idx, w, *nv_stacks)
     except Exception as exc:
         out["experts_nvfp4"] = f"{type(exc).__name__}: {exc}"[:200]
     try:
-        from janus_amd import synth
-        from janus_amd.block import NVFP4SparseMoeBlock
-
         nv = NVFP4SparseMoeBlock.from_tensors(synth.nvfp4_layer(cfg, device=dev), cfg.k)
-        run("block_nvfp4", lambda: nv(x))
-        del nv
+        cases["block_nvfp4"] = lambda: nv(x)
     except Exception as exc:
         out["block_nvfp4"] = f"{type(exc).__name__}: {exc}"[:200]
+
+    times = {name: [] for name in cases}
+    for _ in range(rounds):
+        for name, fn in cases.items():
+            if name in out:
+                continue
+            try:
+                with torch.no_grad():
+                    times[name].append(_time_us(fn))
+            except Exception as exc:  # an extra line of evidence must not take the headline measurement with it
+                out[name] = f"{type(exc).__name__}: {exc}"[:200]
+    for name, ts in times.items():
+        if name not in out:
+            out[name] = float(np.median(ts))
     return out
 
 

@@ -72,6 +72,7 @@ struct ExpertsWorkspace {
   float* slot_scale;  // [T, nslots, H / kSlotBlock] their block scales
   int* sched;       // [nsched] counters of the persistent GEMM launch, cleared by align
   int P, C, nslots, nsched;
+  int chunk_rows;  // chunk_rows_for the call
 };
 
 // plan_block > 0: the permuted rows follow a caller's tile plan padded to that block (align() at that block size).
@@ -79,12 +80,13 @@ ExpertsWorkspace carve_experts(Carver& c, int T, int top_k, int E, int H, int I,
   ExpertsWorkspace w;
   const int A = T * top_k;
   w.P = plan_block > 0 ? ceil_div(A + E * (plan_block - 1), plan_block) * plan_block : A + E * (kRowPad - 1);
-  w.C = ceil_div(A, kChunkRows) + E;
+  w.chunk_rows = chunk_rows_for(A, E);
+  w.C = ceil_div(A, w.chunk_rows) + E;
   w.align = carve_align(c, A, E);
   w.sorted_ids = c.take<int>(w.P);
   w.chunks = c.take<int4>(w.C);
   w.num_chunks = c.take<int>(1);
-  w.nsched = sched_words(w.C, I_s > 0 ? ceil_div(T, kChunkRows) : 0);
+  w.nsched = sched_words(w.C, I_s > 0 ? ceil_div(T, w.chunk_rows) : 0);
   w.sched = c.take<int>(w.nsched);
   w.h = c.take<uint16_t>((size_t)w.P * I);
   w.h_sh = c.take<uint16_t>((size_t)T * I_s);
@@ -139,9 +141,9 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   // the status word, and its slot skipped by the combine. The block path routes padding tokens to id E on purpose.
   int rc = plan_sorted_ids
                ? launch_plan_chunks(plan_sorted_ids, plan_expert_ids, w.P / plan_block, plan_block, A, E, w.sorted_ids,
-                                    w.chunks, w.C, kChunkRows, w.num_chunks, w.sched, w.nsched, stream)
+                                    w.chunks, w.C, w.chunk_rows, w.num_chunks, w.sched, w.nsched, stream)
                : launch_align<IdxT, int>(idx, A, E, kRowPad, w.align, w.sorted_ids, w.P, nullptr, 0, nullptr, w.chunks,
-                                         kChunkRows, w.num_chunks, w.sched, w.nsched, check_ids ? status : nullptr,
+                                         w.chunk_rows, w.num_chunks, w.sched, w.nsched, check_ids ? status : nullptr,
                                          stream);
   if (rc) return rc;
   const bool shared = I_s > 0;
@@ -154,7 +156,8 @@ int run_experts(const uint16_t* x, const IdxT* idx, const float* route_w, const 
   p.num_chunks = w.num_chunks;
   p.codec = codec;
   p.max_chunks = w.C;
-  p.n_shared_chunks = shared ? ceil_div(T, kChunkRows) : 0;
+  p.n_shared_chunks = shared ? ceil_div(T, w.chunk_rows) : 0;
+  p.chunk_rows = w.chunk_rows;
   // gate_up
   p.a = x;
   p.a_bytes = (uint32_t)((size_t)T * H * 2);

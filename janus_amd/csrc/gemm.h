@@ -9,6 +9,11 @@ constexpr int kRowBlocks = 6;                 // MFMA row blocks per workgroup t
 constexpr int kChunkRows = 16 * kRowBlocks;   // rows of one expert (or shared-expert tokens) per workgroup
 constexpr int kRowPad = 16;                   // every expert's rows start at a multiple of this in the permuted order
 
+// Rows per chunk for a call: 96 (the 6-row-block tile), or 16 (a one-row-block tile, three workgroups per CU) when the
+// assignments average at most 4 rows per expert, where nearly every expert fits one 16-row chunk and the launch is
+// bound by the weight decode rather than by MFMA (the shorter tile frees the accumulator registers for more waves).
+inline int chunk_rows_for(long assignments, int E) { return assignments <= 4l * E ? 16 : kChunkRows; }
+
 // Slots: each weighted expert output row (one token, one top-k slot; slot top_k is the gated shared expert) is kept
 // as int16 codes with one fp32 scale per block of kSlotBlock columns, value = code * scale. The down epilogue maps
 // the block's largest |value| to code 32767, so a value's error is at most scale / 2 (2^-16 of the block maximum).
@@ -46,7 +51,8 @@ struct GemmParams {
   const int4* chunks;         // (expert, first position, rows, 0)
   const int* num_chunks;      // device count of valid chunks
   int max_chunks;             // chunk list capacity (grid size)
-  int n_shared_chunks;        // ceil(T / kChunkRows) when the shared expert runs
+  int n_shared_chunks;        // ceil(T / chunk_rows) when the shared expert runs
+  int chunk_rows;             // rows per chunk: 16 * kRowBlocks, or 16 (chunk_rows_for)
   int nslab;                  // column slabs per chunk
   uint16_t* h;                // gate_up output, routed rows [P, N/2]
   uint16_t* h_sh;             // gate_up output, shared rows [T, N_sh/2]

@@ -30,7 +30,8 @@ constexpr int kColBlocks = 4;
 constexpr int KS = 128;                                      // k per pipeline stage: one scale group
 constexpr int kStages = 3;                                   // activation and weight rings: loads run two stages ahead
 constexpr int kRowBytes = KS * 2;                            // one activation row of a stage (bf16)
-constexpr int kSlotBytes = kChunkRows * kRowBytes;           // one LDS activation buffer
+template <int RB>
+constexpr int slot_bytes() { return 16 * RB * kRowBytes; }  // one LDS activation buffer of an RB-row-block tile
 
 enum { kGateUp = 0, kDown = 1 };
 
@@ -193,7 +194,17 @@ struct LdsRing {
   }
 };
 
-template <int MODE, int NKB, int CODEC>
+// An empty asm that takes every activation and weight fragment of a 32-k step at one point (see compute).
+__device__ __forceinline__ void pin_fragments(bf16x8 (&a)[6], bf16x8 (&b)[kColBlocks]) {
+  static_assert(kColBlocks == 4, "the asm lists every fragment");
+  asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(b[0]), "+v"(b[1]),
+                    "+v"(b[2]), "+v"(b[3]));
+}
+__device__ __forceinline__ void pin_fragments(bf16x8 (&a)[1], bf16x8 (&b)[kColBlocks]) {
+  asm volatile("" : "+v"(a[0]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+}
+
+template <int MODE, int NKB, int CODEC, int RB>
 __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams& p, int c, int slab,
                                                                 LdsRing lds, bool poison = false) {
   using C = Codec<CODEC>;
@@ -210,8 +221,8 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   const unsigned char* wsc;
   const float* wgl = nullptr;  // NVFP4: global scale of each weight row
   if (shared) {
-    pos0 = c * kChunkRows;
-    rows = min(kChunkRows, p.T - pos0);
+    pos0 = c * (16 * RB);
+    rows = min((16 * RB), p.T - pos0);
     wq = p.q_sh;
     wsc = reinterpret_cast<const unsigned char*>(p.s_sh);
     if (CODEC == kNvfp4) wgl = p.gsc_sh;
@@ -260,20 +271,22 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   constexpr uint32_t kOutside = 0x80000000u;  // past every activation buffer
   const int lrow = 4 * wave + (lane >> 4);    // this lane's row within a load's 16 (row & 15 of every row it loads)
   const uint32_t achunk = (uint32_t)(((lane & 15) ^ lrow) * 16);
+  // sized for the largest tile (a size that depends on RB trips the host compiler on the buffer-load builtin below);
+  // entries past RB are never read
   uint32_t aoff[kRowBlocks];
   if (MODE == kGateUp && !shared) {
-    int id[kRowBlocks];
+    int id[RB];
 #pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r) {
+    for (int r = 0; r < RB; ++r) {
       const int row = 16 * r + lrow;
       id[r] = p.sorted_ids[pos0 + (row < rows ? row : 0)];
     }
 #pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r)
+    for (int r = 0; r < RB; ++r)
       aoff[r] = (16 * r + lrow < rows) ? (uint32_t)(id[r] / p.topk) * (uint32_t)(K * 2) + achunk : kOutside;
   } else {
 #pragma unroll
-    for (int r = 0; r < kRowBlocks; ++r) {
+    for (int r = 0; r < RB; ++r) {
       const int row = 16 * r + lrow;
       aoff[r] = row < rows ? (uint32_t)(pos0 + row) * (uint32_t)(K * 2) + achunk : kOutside;
     }
@@ -300,9 +313,9 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     gq[cb] = CODEC == kNvfp4 ? wgl[n] : 0.0f;
   }
 
-  f32x4 acc[kRowBlocks][kColBlocks];
+  f32x4 acc[RB][kColBlocks];
 #pragma unroll
-  for (int rb = 0; rb < kRowBlocks; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -324,7 +337,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   // the CU's address unit, which the GEMM keeps busy); their LDS rows otherwise keep older data, read but never
   // multiplied. They are issued first in a stage's group, so the waits the compiler derives for the paths that skip
   // them (fewer loads in flight) cost at most those two early loads on the paths that issue them.
-  constexpr int kAlwaysRb = 4;
+  constexpr int kAlwaysRb = RB < 4 ? RB : 4;
   const int unrb = __builtin_amdgcn_readfirstlane(nrb);
   auto issue_a = [&](auto slot_c, int kb) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
@@ -334,7 +347,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
                                                kb * (KS * 2), 0, 0);
     };
 #pragma unroll
-    for (int r = kAlwaysRb; r < kRowBlocks; ++r)
+    for (int r = kAlwaysRb; r < RB; ++r)
       if (r < unrb) load(r);
 #pragma unroll
     for (int r = 0; r < kAlwaysRb; ++r) load(r);
@@ -398,20 +411,17 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       // copies of its first row, so the reads are defined); only the chunk's row blocks are multiplied. An empty asm
       // takes the activation fragments together with the decoded weights, so the compiler can neither sink a read into
       // its row block's branch, next to its first use, nor hoist the wait for the reads above the decode.
-      bf16x8 afrag[kRowBlocks];
+      bf16x8 afrag[RB];
 #pragma unroll
-      for (int rb = 0; rb < kRowBlocks; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
         afrag[rb] = *reinterpret_cast<const bf16x8*>(base + (16 * rb + nl) * kRowBytes + ((4 * g + t) ^ nl) * 16);
       __builtin_amdgcn_sched_barrier(0);  // the reads issue before the decode
       bf16x8 bfrag[kColBlocks];
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = C::decode(bw[slot][cb][t], scl[cb], t);
-      static_assert(kRowBlocks == 6 && kColBlocks == 4, "the asm below lists every fragment");
-      asm volatile(""
-                   : "+v"(afrag[0]), "+v"(afrag[1]), "+v"(afrag[2]), "+v"(afrag[3]), "+v"(afrag[4]), "+v"(afrag[5]),
-                     "+v"(bfrag[0]), "+v"(bfrag[1]), "+v"(bfrag[2]), "+v"(bfrag[3]));
+      pin_fragments(afrag, bfrag);
 #pragma unroll
-      for (int rb = 0; rb < kRowBlocks; ++rb) {
+      for (int rb = 0; rb < RB; ++rb) {
         if (rb < nrb) {
 #pragma unroll
           for (int cb = 0; cb < kColBlocks; ++cb)
@@ -423,20 +433,20 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   // down: each row's assignment id (the token, for the shared expert) and its routing weight, for the epilogue. The
   // ids are loaded ahead of the second-to-last stage and the weights, which need them, ahead of the last, so neither
   // waits after the k loop. (Rows past the chunk read its first row's: loads without a branch, values not used.)
-  int id[kRowBlocks];
-  float wt[kRowBlocks];
+  int id[RB];
+  float wt[RB];
   auto before = [&](int kb) __attribute__((always_inline)) {
     if constexpr (MODE == kDown) {
       if (kb == (nkb >= 2 ? nkb - 2 : 0)) {
 #pragma unroll
-        for (int rb = 0; rb < kRowBlocks; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
           const int m = rb * 16 + nl;
           id[rb] = shared ? pos0 + (m < rows ? m : 0) : p.sorted_ids[pos0 + (m < rows ? m : 0)];
         }
       }
       if (kb == nkb - 1) {
 #pragma unroll
-        for (int rb = 0; rb < kRowBlocks; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
           wt[rb] = shared ? (p.gamma ? p.gamma[id[rb]] : 1.0f) : p.route_w[id[rb]];
       }
     }
@@ -450,7 +460,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     uint16_t* hbase = shared ? p.h_sh : p.h;
     const int hw = N / 2;
 #pragma unroll
-    for (int rb = 0; rb < kRowBlocks; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
       const int m = rb * 16 + nl;
       if (rb >= nrb || m >= rows) continue;
       uint16_t* hrow = hbase + (long)(pos0 + m) * hw;
@@ -473,16 +483,16 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   } else {
     // each row's slot offset, before the first store (a divisor constant the compiler keeps in scratch would
     // otherwise be reloaded, and waited for, between the stores)
-    long orow_off[kRowBlocks];
+    long orow_off[RB];
 #pragma unroll
-    for (int rb = 0; rb < kRowBlocks; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
       const int tok = shared ? id[rb] : id[rb] / p.topk;
       const int slot = shared ? p.topk : id[rb] - tok * p.topk;
       orow_off[rb] = ((long)tok * p.nslots + slot) * N;
     }
     if (poison) {  // this unit's h rows were not known to be complete: its rows become NaN instead of wrong values
 #pragma unroll
-      for (int rb = 0; rb < kRowBlocks; ++rb) wt[rb] = __builtin_nanf("");
+      for (int rb = 0; rb < RB; ++rb) wt[rb] = __builtin_nanf("");
     }
     // Slot encoding of a row's 64 columns (this wave's block): the 4 lanes of the row (g = 0..3) share the largest
     // |acc|; code = rint(acc * sign(w) * 32767 / max|acc|), scale = |w| max|acc| / 32767 (NaN with w, for a poisoned
@@ -491,9 +501,9 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     // column blocks 0, 1 as stored groups 2g, 2g + 1 and its blocks 2, 3 as 8 + 2g, 9 + 2g (slot_stored_group), so
     // every store instruction writes 64 contiguous bytes per row. The maxima are taken for every row block before the
     // first branch: the cross-lane reads need all lanes.
-    float amax[kRowBlocks];
+    float amax[RB];
 #pragma unroll
-    for (int rb = 0; rb < kRowBlocks; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
       float a = 0.f;
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb)
@@ -504,7 +514,7 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     }
     constexpr float kRound = 12582912.0f;  // 1.5 * 2^23
 #pragma unroll
-    for (int rb = 0; rb < kRowBlocks; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
       const int m = rb * 16 + nl;
       if (rb >= nrb || m >= rows) continue;
       const float w = wt[rb];
@@ -527,14 +537,20 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
 
 // One launch per GEMM: workgroup ids are dealt to the 8 XCDs round-robin, and the slabs of chunk c go to ids on XCD
 // c mod 8, so they share its L2.
-template <int MODE, int NKB, int CODEC>
-__global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParams p) {
+// Workgroups per CU: two for the 96-row tile, three for the 16-row tile (fewer accumulator registers).
+template <int RB>
+constexpr int wg_per_cu() { return RB == 1 ? 3 : 2; }
+
+template <int MODE, int NKB, int CODEC, int RB>
+__global__ void __launch_bounds__(kThreads, wg_per_cu<RB>()) w4a16_gemm_kernel(const GemmParams p) {
   static_assert(kStages == 3, "one array per ring slot");
+  constexpr int kSlotBytes = slot_bytes<RB>();
   __shared__ __attribute__((aligned(16))) unsigned char lds0[kSlotBytes], lds1[kSlotBytes], lds2[kSlotBytes];
+  const LdsRing lds{lds0, lds1, lds2};
   const int xcd = blockIdx.x & 7, within = blockIdx.x >> 3;
   const int c = (within / p.nslab) * 8 + xcd;
   if (c >= p.n_shared_chunks + p.max_chunks) return;
-  gemm_unit<MODE, NKB, CODEC>(p, c, within % p.nslab, LdsRing{lds0, lds1, lds2});
+  gemm_unit<MODE, NKB, CODEC, RB>(p, c, within % p.nslab, lds);
 }
 
 // Both GEMMs in one persistent launch of two workgroups per CU. The work units sit in one queue per XCD: queue q holds
@@ -550,11 +566,14 @@ __global__ void __launch_bounds__(kThreads, 2) w4a16_gemm_kernel(const GemmParam
 constexpr int kSchedQueues = 8;   // ticket counters, one per XCD
 constexpr int kXccIdReg = 20 | (0 << 6) | ((16 - 1) << 11);  // s_getreg operand: HW_REG_XCC_ID, bits 0..15
 
-template <int NKB_GU, int NKB_DN, int CODEC>
-__global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmParams gu, const GemmParams dn,
-                                                                  int* __restrict__ sched, int nq, int spin_limit,
-                                                                  int* __restrict__ status) {
+template <int NKB_GU, int NKB_DN, int CODEC, int RB>
+__global__ void __launch_bounds__(kThreads, wg_per_cu<RB>()) moe_experts_kernel(const GemmParams gu,
+                                                                                 const GemmParams dn,
+                                                                                 int* __restrict__ sched, int nq,
+                                                                                 int spin_limit,
+                                                                                 int* __restrict__ status) {
   static_assert(kStages == 3, "one array per ring slot");
+  constexpr int kSlotBytes = slot_bytes<RB>();
   __shared__ __attribute__((aligned(16))) unsigned char lds0[kSlotBytes], lds1[kSlotBytes], lds2[kSlotBytes];
   const LdsRing lds{lds0, lds1, lds2};
   __shared__ int ticket, gave_up;
@@ -586,7 +605,7 @@ __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmPara
     if (first_wave) next = bump(q);
     if (t < ngu) {
       const int c = __builtin_amdgcn_readfirstlane(q + nq * (t / gu.nslab));
-      gemm_unit<kGateUp, NKB_GU, CODEC>(gu, c, t % gu.nslab, lds);
+      gemm_unit<kGateUp, NKB_GU, CODEC, RB>(gu, c, t % gu.nslab, lds);
       // every wave's h stores have reached the L2 before the count that publishes them
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -611,7 +630,7 @@ __global__ void __launch_bounds__(kThreads, 2) moe_experts_kernel(const GemmPara
         gave_up = give_up;
       }
       __syncthreads();
-      gemm_unit<kDown, NKB_DN, CODEC>(dn, c, u % dn.nslab, lds, __builtin_amdgcn_readfirstlane(gave_up) != 0);
+      gemm_unit<kDown, NKB_DN, CODEC, RB>(dn, c, u % dn.nslab, lds, __builtin_amdgcn_readfirstlane(gave_up) != 0);
     }
     if (first_wave) ticket = __builtin_amdgcn_readfirstlane(next);
     __syncthreads();
@@ -724,13 +743,24 @@ int launch_gemm(const GemmParams& params, hipStream_t stream) {
   JANUS_REQUIRE(p.codec == kInt4 || (p.codec == kNvfp4 && p.gsc && (p.n_shared_chunks == 0 || p.gsc_sh)),
                 JANUS_MOE_EINVAL, "grouped GEMM: codec %d (NVFP4 needs global scales, the shared expert's too)",
                 p.codec);
-#define JANUS_GEMM_CASES(CODEC)                                                                          \
-  switch (nkb) {                                                                                        \
-    case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2, CODEC>), g, b, 0, stream, p); break;         \
-    case 4: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 4, CODEC>), g, b, 0, stream, p); break;         \
-    case 8: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 8, CODEC>), g, b, 0, stream, p); break;         \
-    case 16: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 16, CODEC>), g, b, 0, stream, p); break;       \
-    default: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 0, CODEC>), g, b, 0, stream, p); break;        \
+  JANUS_REQUIRE(p.chunk_rows == 16 * kRowBlocks || p.chunk_rows == 16, JANUS_MOE_EINVAL,
+                "grouped GEMM: chunk_rows=%d (16 or %d)", p.chunk_rows, 16 * kRowBlocks);
+  // the 16-row tile keeps the unrolled k loops of the 35B-A3B shapes (K = 2048 and 512) and the runtime-K loop
+#define JANUS_GEMM_CASES(CODEC)                                                                                \
+  if (p.chunk_rows == 16) {                                                                                   \
+    switch (nkb) {                                                                                            \
+      case 4: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 4, CODEC, 1>), g, b, 0, stream, p); break;          \
+      case 16: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 16, CODEC, 1>), g, b, 0, stream, p); break;        \
+      default: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 0, CODEC, 1>), g, b, 0, stream, p); break;         \
+    }                                                                                                         \
+  } else {                                                                                                    \
+    switch (nkb) {                                                                                            \
+      case 2: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 2, CODEC, kRowBlocks>), g, b, 0, stream, p); break;   \
+      case 4: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 4, CODEC, kRowBlocks>), g, b, 0, stream, p); break;   \
+      case 8: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 8, CODEC, kRowBlocks>), g, b, 0, stream, p); break;   \
+      case 16: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 16, CODEC, kRowBlocks>), g, b, 0, stream, p); break; \
+      default: hipLaunchKernelGGL((w4a16_gemm_kernel<MODE, 0, CODEC, kRowBlocks>), g, b, 0, stream, p); break;  \
+    }                                                                                                         \
   }
   if (p.codec == kNvfp4) {
     JANUS_GEMM_CASES(kNvfp4)
@@ -778,20 +808,30 @@ int launch_experts_fused(const GemmParams& gu_in, const GemmParams& dn_in, int* 
   gu.nslab = ceil_div(max(gu.N, gu.N_sh) / 2, slab_cols<kGateUp>());
   dn.nslab = ceil_div(max(dn.N, dn.N_sh), slab_cols<kDown>());
   const int nkb_gu = gu.K / KS, nkb_dn = dn.K / KS;
-  const dim3 g((unsigned)(2 * d.cus)), b(kThreads);
+  const bool small = gu.chunk_rows == 16;
+  const dim3 g((unsigned)((small ? wg_per_cu<1>() : wg_per_cu<kRowBlocks>()) * d.cus)), b(kThreads);
   // polls of about 1 us: a wait lasts at most one gate_up unit. JANUS_MOE_SPIN_LIMIT (a count, 0 = give up at once)
   // lets a test force the give-up path from the host.
   int spin_limit = 1 << 18;
   if (const char* lim = getenv("JANUS_MOE_SPIN_LIMIT")) spin_limit = atoi(lim) < 0 ? 0 : atoi(lim);
-  if (gu.codec == kInt4 && nkb_gu == 16 && nkb_dn == 4)
-    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kInt4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
+  const bool nv_ok = gu.codec == kNvfp4 && gu.gsc && dn.gsc && (gu.n_shared_chunks == 0 || (gu.gsc_sh && dn.gsc_sh));
+#define JANUS_EXPERTS(GU, DN, CODEC, RB) \
+  hipLaunchKernelGGL((moe_experts_kernel<GU, DN, CODEC, RB>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status)
+  if (small && gu.codec == kInt4 && nkb_gu == 16 && nkb_dn == 4)
+    JANUS_EXPERTS(16, 4, kInt4, 1);
+  else if (small && nv_ok && nkb_gu == 16 && nkb_dn == 4)
+    JANUS_EXPERTS(16, 4, kNvfp4, 1);
+  else if (small)
+    return kNotFused;
+  else if (gu.codec == kInt4 && nkb_gu == 16 && nkb_dn == 4)
+    JANUS_EXPERTS(16, 4, kInt4, kRowBlocks);
   else if (gu.codec == kInt4 && nkb_gu == 4 && nkb_dn == 2)
-    hipLaunchKernelGGL((moe_experts_kernel<4, 2, kInt4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
-  else if (gu.codec == kNvfp4 && gu.gsc && dn.gsc && (gu.n_shared_chunks == 0 || (gu.gsc_sh && dn.gsc_sh)) &&
-           nkb_gu == 16 && nkb_dn == 4)
-    hipLaunchKernelGGL((moe_experts_kernel<16, 4, kNvfp4>), g, b, 0, stream, gu, dn, sched, nq, spin_limit, status);
+    JANUS_EXPERTS(4, 2, kInt4, kRowBlocks);
+  else if (nv_ok && nkb_gu == 16 && nkb_dn == 4)
+    JANUS_EXPERTS(16, 4, kNvfp4, kRowBlocks);
   else
     return kNotFused;
+#undef JANUS_EXPERTS
   JANUS_LAUNCH_CHECK("w4a16 experts");
   return JANUS_MOE_OK;
 }
