@@ -521,6 +521,24 @@ def test_fused_moe_nvfp4_reference_test(gpu, S):
     assert_layer_close(bf16_np(out), _nvfp4_oracle(x, index, weights, st), f"nvfp4 S={S}")
 
 
+@pytest.mark.parametrize("S,E,H,I,k", [(257, 60, 1024, 384, 6), (1, 20, 640, 128, 3), (33, 8, 256, 256, 1)])
+def test_fused_moe_general_shapes(gpu, S, E, H, I, k):
+    """Shapes off the 35B-A3B grid, both codecs against the oracle: a top-k that is not a power of two, E not a
+    multiple of 16, k ranges of 5 and 8 stages (the GEMMs' runtime-K loop, one launch per GEMM), I of one and three
+    column slabs, a single token and top-1."""
+    out, ref = _experts_case(gpu, S, E, H, I, k, seed=S + E, hot=S > 2)
+    assert_layer_close(out, ref, f"int4 S={S} E={E} H={H} I={I} k={k}")
+    st = tuple(t.to(gpu) for t in _nvfp4_stacks(E, I, H, seed=S))
+    g = torch.Generator().manual_seed(S * 7 + k)
+    x = (torch.randn(S, H, generator=g) * 0.5).bfloat16().to(gpu)
+    index = torch.randint(0, E, (S, k), generator=g).to(gpu)
+    weights = torch.softmax(torch.randn(S, k, generator=g), -1).to(gpu)
+    with torch.no_grad():
+        out = fused_moe(x, index, weights, *st)
+    assert_layer_close(bf16_np(out), _nvfp4_oracle(x, index, weights, st), f"nvfp4 S={S} E={E} H={H} I={I} k={k}")
+    ops.check_device_status(gpu)
+
+
 def test_fused_moe_nvfp4_graph_replay(gpu):
     """The reference test's graph check: warm-up on a side stream, capture, replay equals the eager result."""
     E, I, H = 16, 512, 2048
