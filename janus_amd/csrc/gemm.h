@@ -63,11 +63,14 @@ struct GemmParams {
   const float* gamma;         // down: shared-expert weight per token [T], null = 1
 };
 
-// Scheduler words of the persistent launch, zero before it (the align launch clears them): 8 ticket counters, 8 words
-// kept free, then one done counter per chunk.
+// Scheduler words of the persistent launch, zero before it (the align launch clears them): 8 ticket counters, 8 ready
+// counters (one per queue), one done counter per chunk, then per queue (up to 8, each ceil(chunks / queues) long) the
+// list of its chunks whose gate_up units have all finished, in the order they finished (chunk + 1; 0: not yet; kept
+// by the 16-row tile's launch).
 constexpr int kSchedWordsFixed = 16;
+constexpr int kReadyWord = 8;
 __host__ __device__ inline int sched_words(int max_chunks, int n_shared_chunks) {
-  return kSchedWordsFixed + max_chunks + n_shared_chunks;
+  return kSchedWordsFixed + 2 * (max_chunks + n_shared_chunks) + 8;
 }
 constexpr int kNotFused = 1;  // launch_experts_fused: no persistent kernel for these sizes (or JANUS_MOE_SCHEDULE=split)
 

@@ -561,11 +561,18 @@ __global__ void __launch_bounds__(kThreads, wg_per_cu<RB>()) w4a16_gemm_kernel(c
 // With the 96-row tile queue q holds a contiguous range of chunks: the chunks of one expert (or of the shared expert)
 // then mostly share an L2 and read its weights from HBM once (T=16384: 1129 -> 1109 us, T=2048: 215 -> 212 us). The
 // 16-row tile deals chunks c = q, q + nq, ... instead, which measured 11% faster at T=96 than the contiguous ranges.
-// A down unit waits until all gate_up units of its chunk have counted themselves done. It never waits for a unit
-// without a workgroup: each gate_up unit it depends on has a lower ticket of the same queue, so a running workgroup
-// took it, and gate_up units wait for nothing. The wait is bounded: after spin_limit polls (0: none) it gives up, sets
-// kStatusGaveUp in the device status word and writes NaN for its rows instead of a result computed on h rows that may
-// be incomplete; the launch still ends.
+// A down unit waits until all gate_up units of its chunk have counted themselves done. With the 96-row tile, down
+// ticket u belongs to the queue's chunk u / slabs in list order. With the 16-row tile the chunks go in the order their
+// gate_up units finish: the gate_up unit that completes a chunk (the last of its slabs to count itself done) appends
+// it to the queue's ready list, and down ticket u takes the chunk at position u / slabs of that list, waiting until it
+// is written, so it waits for whichever chunk finishes next rather than one particular chunk. At T=96 gate_up units
+// of equal work take 28-77 us and the fixed order left down units waiting for the slowest (launch 123.0 -> 115.4 us);
+// with the 96-row tile the ready list measured the same at T=2048 and 1.5% slower at T=16384. Either way a down unit
+// never waits for a unit without a workgroup: every gate_up unit of the queue has a lower ticket, so a running
+// workgroup took it, and gate_up units wait for nothing; they all finish, and every chunk enters the list. The wait is
+// bounded: after spin_limit polls (0: none) it gives up, sets kStatusGaveUp in the device status word and (16-row
+// tile) takes the chunk of the list order, writing NaN for its rows instead of a result computed on h rows that may be
+// incomplete; the launch still ends.
 constexpr int kSchedQueues = 8;   // ticket counters, one per XCD
 constexpr int kXccIdReg = 20 | (0 << 6) | ((16 - 1) << 11);  // s_getreg operand: HW_REG_XCC_ID, bits 0..15
 
@@ -579,7 +586,7 @@ __global__ void __launch_bounds__(kThreads, wg_per_cu<RB>()) moe_experts_kernel(
   constexpr int kSlotBytes = slot_bytes<RB>();
   __shared__ __attribute__((aligned(16))) unsigned char lds0[kSlotBytes], lds1[kSlotBytes], lds2[kSlotBytes];
   const LdsRing lds{lds0, lds1, lds2};
-  __shared__ int ticket, gave_up;
+  __shared__ int ticket, gave_up, down_chunk;
   // Every branch of this loop is uniform over a wave: wave 0 does the bookkeeping with all its lanes. A branch on the
   // thread id would give the loop a per-lane exit, and the compiler may then run the other lanes around the loop ahead
   // of lane 0, through barriers, on a stale ticket. The counters are bumped by buffer atomics that only lane 0 keeps
@@ -593,13 +600,14 @@ __global__ void __launch_bounds__(kThreads, wg_per_cu<RB>()) moe_experts_kernel(
     return __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, srsrc, lane0 ? word * 4 : 0x7FFFFFF0, 0, 0);
   };
   const int q = (int)(__builtin_amdgcn_s_getreg(kXccIdReg) & 0xF) % nq;
-  const int* done = sched + kSchedWordsFixed;  // per chunk c
   const int total = gu.n_shared_chunks + *gu.num_chunks;
   // this queue's chunks: c0, c0 + cstep, ... (ncq of them)
   const int c0 = RB == 1 ? q : (int)((long)q * total / nq);
   const int cstep = RB == 1 ? nq : 1;
   const int ncq = RB == 1 ? (total > q ? (total - q + nq - 1) / nq : 0) : (int)((long)(q + 1) * total / nq) - c0;
   const int ngu = ncq * gu.nslab, nall = ngu + ncq * dn.nslab;
+  const int total_max = gu.n_shared_chunks + gu.max_chunks;
+  const int ready_word = kSchedWordsFixed + total_max + q * ((total_max + nq - 1) / nq);  // this queue's ready list
   if (first_wave) ticket = __builtin_amdgcn_readfirstlane(bump(q));
   __syncthreads();
   int t = __builtin_amdgcn_readfirstlane(ticket);
@@ -615,27 +623,47 @@ __global__ void __launch_bounds__(kThreads, wg_per_cu<RB>()) moe_experts_kernel(
       // every wave's h stores have reached the L2 before the count that publishes them
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (first_wave) (void)bump(kSchedWordsFixed + c);
+      if (first_wave) {
+        const int old = __builtin_amdgcn_readfirstlane(bump(kSchedWordsFixed + c));
+        if (RB == 1 && old == gu.nslab - 1) {  // the chunk's last gate_up unit: append the chunk to the ready list
+          const int pos = __builtin_amdgcn_readfirstlane(bump(kReadyWord + q));
+          // the list word is still zero: adding c + 1 writes it
+          (void)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(c + 1, srsrc, lane0 ? (ready_word + pos) * 4 : 0x7FFFFFF0,
+                                                               0, 0);
+        }
+      }
     } else {
       const int u = t - ngu;
-      const int c = __builtin_amdgcn_readfirstlane(c0 + cstep * (u / dn.nslab));
+      const int idx = u / dn.nslab;  // the chunk at this position of the ready list
       if (first_wave) {
-        int give_up = 0;
+        int give_up = 0, entry = 0;
         for (int spins = 0;; ++spins) {
           if (spins >= spin_limit) {
             give_up = 1;
             if (lane0) __hip_atomic_fetch_or(status, kStatusGaveUp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
-          const int n = __builtin_amdgcn_readfirstlane(
-              __hip_atomic_load(done + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-          if (n >= gu.nslab) break;
+          if (RB == 1) {
+            entry = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(sched + ready_word + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            if (entry > 0) break;
+          } else {
+            const int fixed = c0 + cstep * idx;
+            const int n = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(sched + kSchedWordsFixed + fixed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            if (n >= gu.nslab) {
+              entry = fixed + 1;
+              break;
+            }
+          }
           __builtin_amdgcn_s_sleep(2);
         }
         asm volatile("buffer_inv sc0" ::: "memory");  // this CU's L1 drops any stale copy of the chunk's h rows
         gave_up = give_up;
+        down_chunk = give_up ? c0 + cstep * idx : entry - 1;
       }
       __syncthreads();
+      const int c = __builtin_amdgcn_readfirstlane(down_chunk);
       gemm_unit<kDown, NKB_DN, CODEC, RB>(dn, c, u % dn.nslab, lds, __builtin_amdgcn_readfirstlane(gave_up) != 0);
     }
     if (first_wave) ticket = __builtin_amdgcn_readfirstlane(next);
