@@ -293,8 +293,12 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
   }
 
   // ---- weight rows of this lane, one per column block (an idle wave reads row 0 and discards it) ----
-  const unsigned char* wbase = reinterpret_cast<const unsigned char*>(wq);
-  const unsigned char* sbase = wsc;
+  // the unit's weight and scale rows as buffer resources (32-bit lane offsets, the stage's offset an immediate)
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(wq), (short)0, (int)((uint32_t)N * (uint32_t)(K / 2)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srsrc_w = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned char*>(wsc), (short)0, (int)((uint32_t)N * (uint32_t)(K / KS * C::kScaleBytesPerStage)),
+      0x00020000);
   uint32_t woff[kColBlocks], soff[kColBlocks];
   float gq[kColBlocks];
 #pragma unroll
@@ -356,12 +360,13 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int cb = 0; cb < kColBlocks; ++cb) {
-      bw[slot][cb] = *reinterpret_cast<const u32x4*>(wbase + woff[cb] + kb * (KS / 2));
+      bw[slot][cb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, woff[cb], kb * (KS / 2), 0));
       if constexpr (kBatchScales) {
         if (kb % 4 == 0)
-          scb[(kb / 4) & 1][cb] = *reinterpret_cast<const u32x2*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
+          scb[(kb / 4) & 1][cb] = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_raw_buffer_load_b64(srsrc_w, soff[cb], kb * C::kScaleBytesPerStage, 0));
       } else {
-        sc[slot][cb] = *reinterpret_cast<const uint16_t*>(sbase + soff[cb] + kb * C::kScaleBytesPerStage);
+        sc[slot][cb] = __builtin_amdgcn_raw_buffer_load_b16(srsrc_w, soff[cb], kb * C::kScaleBytesPerStage, 0);
       }
     }
   };
@@ -416,6 +421,16 @@ __device__ __attribute__((always_inline)) inline void gemm_unit(const GemmParams
       for (int rb = 0; rb < RB; ++rb)
         afrag[rb] = *reinterpret_cast<const bf16x8*>(base + (16 * rb + nl) * kRowBytes + ((4 * g + t) ^ nl) * 16);
       __builtin_amdgcn_sched_barrier(0);  // the reads issue before the decode
+      if constexpr (RB == 1) {
+        // one row block: each column block's weights are decoded right before their MFMA (one fragment live)
+#pragma unroll
+        for (int cb = 0; cb < kColBlocks; ++cb) {
+          bf16x8 b = C::decode(bw[slot][cb][t], scl[cb], t);
+          asm volatile("" : "+v"(b), "+v"(afrag[0]));
+          acc[0][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, afrag[0], acc[0][cb], 0, 0, 0);
+        }
+        continue;
+      }
       bf16x8 bfrag[kColBlocks];
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; ++cb) bfrag[cb] = C::decode(bw[slot][cb][t], scl[cb], t);
