@@ -671,6 +671,30 @@ def test_nvfp4_block_matches_oracle(gpu, name, monkeypatch):
     ops.check_device_status(gpu)
 
 
+def test_nvfp4_block_headline_matches_oracle_on_sampled_tokens(gpu, monkeypatch):
+    """The NVFP4 layer at T=2048: the 96-row tile's persistent launch with NVFP4 shared chunks. Routing bit-exact on
+    the sampled tokens, output to the layer bar against the oracle on 256 of them (spread over the batch, so over
+    every XCD's chunk range), and the same bits as one launch per GEMM on every token."""
+    cfg = synth.CONFIGS["headline"]
+    L = synth.nvfp4_layer(cfg, device=gpu)
+    blk = NVFP4SparseMoeBlock.from_tensors(L, cfg.k)
+    x = synth.activations(cfg).to(gpu)
+    with torch.no_grad():
+        out, idx, w = _nvfp4_block_call(blk, x)
+        monkeypatch.setenv("JANUS_MOE_SCHEDULE", "split")
+        split, _, _ = _nvfp4_block_call(blk, x)
+        monkeypatch.delenv("JANUS_MOE_SCHEDULE")
+    torch.cuda.synchronize()
+    assert torch.equal(split, out)
+    tokens = np.linspace(0, cfg.T - 1, 256).astype(np.int64)
+    ref, ridx, rw, _ = O.block_forward_nvfp4(O.numpy_layer({k: None if v is None else v.cpu() for k, v in L.items()}),
+                                             bf16_np(x.cpu()), cfg.k, tokens=tokens)
+    assert np.array_equal(idx.cpu().numpy()[tokens], ridx)
+    np.testing.assert_allclose(w.cpu().numpy()[tokens], rw, rtol=1e-4, atol=1e-6)
+    assert_layer_close(bf16_np(out.cpu())[tokens], ref, "nvfp4 headline")
+    ops.check_device_status(gpu)
+
+
 # ---- fused_moe with a reused plan ------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("S,E,H,I,k", [(3, 16, 512, 256, 2), (100, 16, 2048, 512, 8), (700, 16, 2048, 512, 8),
